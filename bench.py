@@ -1,0 +1,198 @@
+#!/usr/bin/env python3
+"""Benchmark of the batched sensor-feature path on one MI355X.
+
+Workload: 16,384 environments per call, each
+4x64x64 uint8 cameras + 4,148-float observation (4,096 LiDAR bins, 52 state
+values) + 10-float mission -> 142 float features.  One "step" is one call of
+tb_cuda_extract_features_device over the whole resident batch; inputs rotate
+over several buffer sets (each 550 MB, together far above the 256 MB
+Infinity Cache) so no step is served from cache.
+
+Prints ONE JSON line (the driver's contract) with a `roofline` object (the
+feature kernel's algorithmic HBM bytes / its average duration, HIP events on
+the launch stream) and a `cpu_baseline` object (the CPU oracle timed on this
+host's cores over a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "sensor-feature envs/sec and achieved HBM GB/s (% of peak) at 16,384 envs"
+BATCH = 16384
+OBS_B, MISSION_B, CAMERA_B, OUT_B = 4148 * 4, 10 * 4, 16384, 142 * 4
+BYTES_PER_ENV = OBS_B + MISSION_B + CAMERA_B + OUT_B          # 33,584 algorithmic bytes
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_features_16384.json"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def host_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def make_sets(torch, nsets: int, threads: int):
+    from turbinator_c_amd import synth
+    sets = []
+    host0 = None
+    for k in range(nsets):
+        b = synth.make_batch(BATCH, seed=42 + k, threads=threads)
+        if k == 0:
+            host0 = b
+        sets.append((torch.from_numpy(b.obs).cuda(), torch.from_numpy(b.mission).cuda(),
+                     torch.from_numpy(b.cameras).cuda(),
+                     torch.empty((BATCH, 142), dtype=torch.float32, device="cuda")))
+    torch.cuda.synchronize()
+    return sets, host0
+
+
+def time_gpu(torch, sets, steps: int, warmup: int):
+    from turbinator_c_amd import features
+    stream = torch.cuda.current_stream()
+    n = len(sets)
+
+    def call(i):
+        o, m, c, out = sets[i % n]
+        if features.extract_features_device(o, m, c, out, BATCH, stream) != 1:
+            raise RuntimeError("tb_cuda_extract_features_device launch failed")
+
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for i in range(steps):
+        call(i)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(stop) / 1e3, wall
+
+
+def verify_sample(torch, sets, host0) -> dict:
+    """Checks the benchmarked set-0 outputs on 256 envs against the oracle."""
+    import oracle
+    from tests.conftest import assert_feature_parity
+    idx = np.linspace(0, BATCH - 1, 256).astype(np.int64)
+    got = sets[0][3].cpu().numpy()[idx]
+    want = oracle.features(host0.obs[idx], host0.mission[idx], host0.cameras[idx])
+    return assert_feature_parity(got, want, "bench-sample")
+
+
+def cpu_baseline(host0, threads: int, budget_s: float) -> dict:
+    """The CPU oracle (restatement of src/training/training.c:102-142,
+    -O3 -std=c11) over the first environments of the same batch, on
+    `threads` host threads, repeated until `budget_s` of wall time."""
+    import oracle
+    lib = oracle.lib()
+    sample = min(BATCH, 4096 * threads)
+    out = np.empty((sample, 142), np.float32)
+    args = (host0.obs.ctypes.data, OBS_B, host0.mission.ctypes.data, MISSION_B,
+            host0.cameras.ctypes.data, CAMERA_B, out.ctypes.data, sample, threads)
+    lib.orc_features_batch(*args)  # warm-up pass
+    envs, t0 = 0, time.perf_counter()
+    while True:
+        lib.orc_features_batch(*args)
+        envs += sample
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    rate = envs / el
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(rate, 1), "unit": "envs/s", "cores": threads, "kind": "port",
+            "sample": f"{envs} envs ({sample}-env slices of the configuration-3 batch, "
+                      f"{el:.1f} s) on {threads} threads of {cpu}; "
+                      f"{rate * BYTES_PER_ENV / 1e9:.2f} GB/s effective"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--sets", type=int, default=3, help="rotating input buffer sets")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the feature path needs no "
+              "inter-GPU exchange; see DESIGN.md for how it shards). Use --gpus 1.",
+              file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    from turbinator_c_amd import features
+    features.hip_lib()
+    threads = host_threads()
+    log(f"[bench] generating {args.sets} x {BATCH} envs on {threads} threads")
+    sets, host0 = make_sets(torch, args.sets, threads)
+    log("[bench] timing")
+    gpu_s, wall_s = time_gpu(torch, sets, args.steps, args.warmup)
+    per_call = gpu_s / args.steps
+    stats = verify_sample(torch, sets, host0)
+    log(f"[bench] parity sample ok: {stats}")
+    bytes_per_call = BYTES_PER_ENV * BATCH
+    achieved = bytes_per_call / per_call / 1e9
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+    cpu = None
+    if not args.no_cpu:
+        log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")
+        cpu = cpu_baseline(host0, threads, args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(BATCH / per_call, 1),
+        "unit": "envs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(per_call * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "configuration 3: 16,384 envs/call, 4x64x64 u8 cameras + "
+                               "4,148 f32 obs + 10 f32 mission -> 142 f32 features",
+                   "global_batch": BATCH, "bytes_per_env": BYTES_PER_ENV,
+                   "buffer_sets": args.sets, "entry": "tb_cuda_extract_features_device",
+                   "wall_s_timed": round(wall_s, 4)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,55 @@
+/*
+ * Extensions of the sensor-feature boundary offered by the gfx950 backend
+ * (libturbinator_hip).  They have no declaration in the reference header
+ * include/turbinator/training/cuda_features.h; each one states the
+ * reference code whose semantics it reuses.  All entries are asynchronous on
+ * `stream` (a hipStream_t as void*, NULL = null stream) and return 1 iff the
+ * launch was accepted, 0 on invalid arguments (nothing is launched then).
+ */
+#ifndef TURBINATOR_HIP_FEATURES_H
+#define TURBINATOR_HIP_FEATURES_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TB_HIP_OBS_DIM = 4148,
+    TB_HIP_MISSION_DIM = 10,
+    TB_HIP_CAMERA_BYTES = 16384,
+    TB_HIP_FEATURE_DIM = 142,
+    TB_HIP_DIAG_WORDS = 224,
+    TB_HIP_TACTICAL_DIM = 24,
+    TB_HIP_PRIOR_DIM = 15,
+    TB_HIP_ONBOARD_DIAG_DIM = 4
+};
+
+/* The 142 features of tb_cuda_extract_features_device (reference
+ * src/cuda/features.cu:158-169 / src/training/training.c:102-142) read in
+ * place from strided records, e.g. the 66,672-byte replay transitions whose
+ * field order is tb_gpu_host_batch (include/turbinator/gpu/replay.h:17-30).
+ * Strides are bytes between consecutive environments.  obs and mission rows
+ * must be 4-byte aligned (base and stride); cameras may have any alignment
+ * and may be NULL (features 126..141 = 0).  features rows are dense
+ * [batch,142].  Returns 0 for NULL obs/mission/features, batch 0 or above
+ * 0x7fffffff, or misaligned float rows. */
+int tb_hip_extract_features_strided_device(const void *obs, size_t obs_stride,
+                                           const void *mission, size_t mission_stride,
+                                           const void *cameras, size_t camera_stride,
+                                           float *features,
+                                           size_t batch_size, void *stream);
+
+/* Per-bin LiDAR transform of the feature kernel, elementwise over `count`
+ * floats: -1 for non-finite or negative ranges, otherwise
+ * log1p(min(r,120)) / log1pf(120) (reference training.c:65-68).  Exposed so
+ * the transform's accuracy can be measured over every float input. */
+int tb_hip_lidar_transform_device(const float *ranges, float *out,
+                                  size_t count, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

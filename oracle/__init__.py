@@ -1,0 +1,121 @@
+"""TEST INFRASTRUCTURE ONLY: Python handle on the CPU checker.
+
+Imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg;
+never by turbinator_c_amd.  Wraps oracle/liboracle.so (restatement of the
+reference algorithms) and, when built, oracle/_ref/libref_training.so (the
+reference's own src/training/training.c).
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_size_t, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_ORACLE = HERE / "liboracle.so"
+LIB_REF = HERE / "_ref" / "libref_training.so"
+
+OBS, MISSION, CAMERA, FEATURES, DIAG_WORDS = 4148, 10, 16384, 142, 224
+
+_orc = None
+_ref = None
+
+
+def lib() -> ctypes.CDLL:
+    global _orc
+    if _orc is None:
+        if not LIB_ORACLE.exists():
+            raise RuntimeError("oracle/liboracle.so not built (make -C oracle)")
+        l = ctypes.CDLL(str(LIB_ORACLE))
+        l.orc_features_env.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p]
+        l.orc_features_env.restype = None
+        l.orc_features_batch.argtypes = [c_void_p, c_size_t, c_void_p, c_size_t, c_void_p,
+                                         c_size_t, c_void_p, c_size_t, c_int]
+        l.orc_features_batch.restype = None
+        l.orc_lidar_feature.argtypes = [c_float]
+        l.orc_lidar_feature.restype = c_float
+        l.orc_lidar_feature_array.argtypes = [c_void_p, c_void_p, c_size_t, c_int]
+        l.orc_lidar_feature_array.restype = None
+        l.orc_depth_to_luma.argtypes = [c_float]
+        l.orc_depth_to_luma.restype = ctypes.c_uint8
+        l.orc_diagnostics_env.argtypes = [c_void_p, c_void_p, c_void_p]
+        l.orc_diagnostics_env.restype = None
+        if hasattr(l, "orc_onboard_env"):
+            l.orc_onboard_env.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
+            l.orc_onboard_env.restype = None
+        _orc = l
+    return _orc
+
+
+def ref_lib() -> ctypes.CDLL | None:
+    """The reference's own training.c, or None when it was not built."""
+    global _ref
+    if _ref is None and LIB_REF.exists():
+        l = ctypes.CDLL(str(LIB_REF))
+        l.tb_train_extract_features_cpu.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p]
+        l.tb_train_extract_features_cpu.restype = None
+        _ref = l
+    return _ref
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def features(obs: np.ndarray, mission: np.ndarray, cameras: np.ndarray | None,
+             threads: int = 8) -> np.ndarray:
+    """[B,142] features of dense [B,4148]/[B,10]/[B,16384] host arrays."""
+    obs = np.ascontiguousarray(obs, np.float32)
+    mission = np.ascontiguousarray(mission, np.float32)
+    if cameras is not None:
+        cameras = np.ascontiguousarray(cameras, np.uint8)
+    b = obs.shape[0]
+    out = np.empty((b, FEATURES), np.float32)
+    lib().orc_features_batch(_p(obs), OBS * 4, _p(mission), MISSION * 4, _p(cameras), CAMERA,
+                             _p(out), b, threads)
+    return out
+
+
+def features_strided(buf: np.ndarray, batch: int, record: int, obs_off: int, mission_off: int,
+                     camera_off: int | None, threads: int = 8) -> np.ndarray:
+    out = np.empty((batch, FEATURES), np.float32)
+    base = buf.ctypes.data
+    lib().orc_features_batch(base + obs_off, record, base + mission_off, record,
+                             None if camera_off is None else base + camera_off, record,
+                             _p(out), batch, threads)
+    return out
+
+
+def reference_features(obs: np.ndarray, mission: np.ndarray,
+                       cameras: np.ndarray | None) -> np.ndarray:
+    """[B,142] from the reference's compiled tb_train_extract_features_cpu."""
+    r = ref_lib()
+    if r is None:
+        raise RuntimeError("oracle/_ref not built")
+    obs = np.ascontiguousarray(obs, np.float32)
+    mission = np.ascontiguousarray(mission, np.float32)
+    out = np.empty((obs.shape[0], FEATURES), np.float32)
+    for e in range(obs.shape[0]):
+        cam = None if cameras is None else cameras[e].ctypes.data
+        r.tb_train_extract_features_cpu(obs[e].ctypes.data, mission[e].ctypes.data, cam,
+                                        out[e].ctypes.data)
+    return out
+
+
+def lidar_feature(values: np.ndarray, threads: int = 8) -> np.ndarray:
+    v = np.ascontiguousarray(values, np.float32)
+    out = np.empty_like(v)
+    lib().orc_lidar_feature_array(_p(v), _p(out), v.size, threads)
+    return out
+
+
+def diagnostics(obs: np.ndarray, cameras: np.ndarray | None) -> np.ndarray:
+    b = obs.shape[0]
+    out = np.empty((b, DIAG_WORDS), np.uint32)
+    for e in range(b):
+        cam = None if cameras is None else np.ascontiguousarray(cameras[e]).ctypes.data
+        lib().orc_diagnostics_env(np.ascontiguousarray(obs[e], np.float32).ctypes.data, cam,
+                                  out[e].ctypes.data)
+    return out

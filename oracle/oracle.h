@@ -1,0 +1,64 @@
+/*
+ * TEST INFRASTRUCTURE ONLY.  CPU restatement of the reference's sensor-feature
+ * algorithms, used by tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg as the checker.  Nothing in turbinator_c_amd/ may link,
+ * load or call it.
+ */
+#ifndef TB_ORACLE_H
+#define TB_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    ORC_OBS = 4148,
+    ORC_MISSION = 10,
+    ORC_CAMERA = 16384,
+    ORC_FEATURES = 142,
+    ORC_DIAG_WORDS = 224
+};
+
+/* One environment, reference src/training/training.c:102-142. */
+void orc_features_env(const float *obs, const float *mission,
+                      const uint8_t *cameras, float *out);
+
+/* Strided batch over `threads` POSIX threads (static env partition).
+ * Strides are in bytes between consecutive environments.  cameras may be
+ * NULL.  out rows are dense [batch,142]. */
+void orc_features_batch(const unsigned char *obs, size_t obs_stride,
+                        const unsigned char *mission, size_t mission_stride,
+                        const unsigned char *cameras, size_t camera_stride,
+                        float *out, size_t batch, int threads);
+
+/* The reference's LiDAR bin transform f(r) (training.c:65-68). */
+float orc_lidar_feature(float range_m);
+
+/* orc_lidar_feature over an array, on `threads` POSIX threads. */
+void orc_lidar_feature_array(const float *in, float *out, size_t n, int threads);
+
+/* Depth (metres) -> luma byte map used for fp32-depth camera inputs. */
+uint8_t orc_depth_to_luma(float depth_m);
+
+/* Per-environment diagnostics with no counterpart in the 142-vector:
+ * words 0..63    LiDAR sector minimum over valid bins (float, -1 if none)
+ * words 64..127  LiDAR argmin bin index 0..4095 (int32, first in scan order, -1)
+ * words 128..191 LiDAR valid-bin count (int32)
+ * words 192..207 camera quadrant minimum byte (int32, 0 when cameras NULL)
+ * words 208..223 camera quadrant occupancy: bytes != 0 (int32)              */
+void orc_diagnostics_env(const float *obs, const uint8_t *cameras, uint32_t *diag);
+
+/* Onboard tactical (24) and prior (15) features, reference
+ * src/network/onboard_features.cuh:25-519.  `diag` (nullable) receives
+ * {min_r, argmin ray (as float), min_dx_c, cluster_count (as float)}. */
+void orc_onboard_env(const float *obs, const float *mission,
+                     float *tactical24, float *prior15, float *diag4);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,73 @@
+"""Shared fixtures and parity helpers.
+
+Tolerance classes of the 142-feature vector (parity bar of the port):
+  exact      features 0..61 (clamps, scan statistics, mission + arena mask)
+             and 126..141 (integer camera sums / 261120): bit-for-bit.
+  tolerance  features 62..125 (LiDAR sector means of log1p):
+             |gpu - cpu| <= 1e-5 * |cpu| + 1e-6.
+"""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+EXACT = np.r_[0:62, 126:142]
+LIDAR = np.arange(62, 126)
+LIDAR_REL_TOL = 1e-5
+LIDAR_ABS_TOL = 1e-6
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+def assert_feature_parity(got: np.ndarray, want: np.ndarray, label: str = "") -> dict:
+    """Checks [B,142] GPU features against the CPU oracle; returns stats."""
+    assert got.shape == want.shape, (got.shape, want.shape)
+    assert np.isfinite(got).all(), f"{label}: non-finite feature"
+    gb = got.view(np.uint32)[:, EXACT]
+    wb = want.view(np.uint32)[:, EXACT]
+    bad = np.argwhere(gb != wb)
+    if bad.size:
+        e, k = bad[0]
+        raise AssertionError(f"{label}: exact feature {EXACT[k]} of env {e} differs: "
+                             f"gpu {got[e, EXACT[k]]!r} cpu {want[e, EXACT[k]]!r} "
+                             f"({len(bad)} mismatches)")
+    g = got[:, LIDAR].astype(np.float64)
+    w = want[:, LIDAR].astype(np.float64)
+    err = np.abs(g - w)
+    lim = LIDAR_REL_TOL * np.abs(w) + LIDAR_ABS_TOL
+    over = np.argwhere(err > lim)
+    if over.size:
+        e, k = over[0]
+        raise AssertionError(f"{label}: LiDAR feature {LIDAR[k]} of env {e}: gpu {g[e, k]!r} "
+                             f"cpu {w[e, k]!r} err {err[e, k]:.3g} > {lim[e, k]:.3g}")
+    # The reference's own cross-check (tests/test_cuda_features.c:43).
+    assert np.abs(got - want).max() <= 2.0e-5
+    rel = err / np.maximum(np.abs(w), 1e-30)
+    return {"lidar_max_abs": float(err.max()), "lidar_max_rel": float(rel[np.abs(w) > 1e-3].max()
+            if (np.abs(w) > 1e-3).any() else 0.0),
+            "lidar_bit_exact_frac": float((got[:, LIDAR].view(np.uint32) ==
+                                           want[:, LIDAR].view(np.uint32)).mean())}
+
+
+@pytest.fixture(scope="session")
+def torch_cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test selected but no GPU is visible")
+    return torch
+
+
+@pytest.fixture(scope="session")
+def hip(torch_cuda):
+    from turbinator_c_amd import features
+    features.hip_lib()  # raises when the HIP library is not built
+    return features

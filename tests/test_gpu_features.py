@@ -1,0 +1,228 @@
+"""GPU parity of the 142-feature path against the CPU oracle, through the C-ABI.
+
+Cases: the reference's 3-env fixture through the host batch object, the
+golden sets, configuration 2 (1,024 envs), configuration 4 (4,096-env edge
+quarters), configuration 3 at its full 16,384 envs, configuration 5's
+66,672-byte replay records (aligned, 4-byte-aligned next_obs and byte-aligned
+cameras), NULL cameras, non-finite inputs, a non-default stream, and the
+reference's own tests/test_cuda_features.c linked against this library.
+Tolerance classes are defined in tests/conftest.py.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.conftest import assert_feature_parity
+from tests.golden.make_golden import fixture_sets
+from turbinator_c_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = np.load(oracle.HERE.parent / "tests" / "golden" / "features_golden.npz")
+
+# Replay transition record, field order of tb_gpu_host_batch
+# (reference include/turbinator/gpu/replay.h:17-30).
+RECORD = 66672
+OFF_OBS, OFF_MISSION, OFF_CAM = 0, 16592, 16632
+OFF_NEXT_OBS, OFF_NEXT_MISSION, OFF_NEXT_CAM = 33396, 49988, 50028
+
+
+def note(msg: str) -> None:
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def run_device(torch, hip, obs, mission, cameras, stream=None):
+    b = obs.shape[0]
+    d_obs = torch.from_numpy(np.ascontiguousarray(obs)).cuda()
+    d_mis = torch.from_numpy(np.ascontiguousarray(mission)).cuda()
+    d_cam = None if cameras is None else torch.from_numpy(np.ascontiguousarray(cameras)).cuda()
+    out = torch.full((b, 142), float("nan"), dtype=torch.float32, device="cuda")
+    s = stream or torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    assert hip.extract_features_device(d_obs, d_mis, d_cam, out, b, s) == 1
+    assert hip.synchronize(s) == 1
+    return out.cpu().numpy()
+
+
+def test_reference_fixture_through_host_object(hip):
+    note("ref3 via tb_cuda_extract_features_host")
+    sets = {n: inputs for n, inputs, _ in fixture_sets()}
+    obs, mission, cams = sets["ref3"]
+    batch = hip.FeatureBatch.create(0, 3)
+    assert batch is not None
+    try:
+        out = np.full((3, 142), np.nan, np.float32)
+        assert batch.extract_host(obs, mission, cams, 3, out) == 1, batch.error()
+        assert batch.error() == ""
+    finally:
+        batch.destroy()
+    stats = assert_feature_parity(out, GOLDEN["ref3"], "ref3")
+    note(f"ref3 stats {stats}")
+
+
+@pytest.mark.parametrize("name", ["c1", "c4", "special"])
+def test_golden_sets_device(torch_cuda, hip, name):
+    note(f"golden {name}")
+    sets = {n: inputs for n, inputs, _ in fixture_sets()}
+    obs, mission, cams = sets[name]
+    got = run_device(torch_cuda, hip, obs, mission, cams)
+    stats = assert_feature_parity(got, GOLDEN[name], name)
+    note(f"{name} stats {stats}")
+
+
+def test_config2_1024_envs(torch_cuda, hip):
+    note("config 2: 1024 envs")
+    b = synth.make_batch(1024, seed=42)
+    got = run_device(torch_cuda, hip, b.obs, b.mission, b.cameras)
+    stats = assert_feature_parity(got, oracle.features(b.obs, b.mission, b.cameras), "c2")
+    note(f"c2 stats {stats}")
+
+
+def test_config4_edge_quarters(torch_cuda, hip):
+    note("config 4: 4096 envs edge quarters")
+    b = synth.make_batch(4096, seed=42, variant=synth.EDGE_QUARTERS)
+    got = run_device(torch_cuda, hip, b.obs, b.mission, b.cameras)
+    want = oracle.features(b.obs, b.mission, b.cameras)
+    stats = assert_feature_parity(got, want, "c4")
+    assert np.all(got[:1024, 62:126] == -1.0)                       # Q1 all no-return
+    assert np.all(got[1024:2048, 126:142] == np.float32(207) / np.float32(255))  # Q2
+    note(f"c4 stats {stats}")
+
+
+def test_config3_full_16384(torch_cuda, hip):
+    note("config 3: 16384 envs full parity")
+    b = synth.make_batch(16384, seed=42, threads=16)
+    got = run_device(torch_cuda, hip, b.obs, b.mission, b.cameras)
+    stats = assert_feature_parity(got, oracle.features(b.obs, b.mission, b.cameras, threads=16),
+                                  "c3")
+    note(f"c3 stats {stats}")
+
+
+def test_null_cameras(torch_cuda, hip):
+    note("NULL cameras")
+    b = synth.make_batch(64, seed=11)
+    got = run_device(torch_cuda, hip, b.obs, b.mission, None)
+    assert_feature_parity(got, oracle.features(b.obs, b.mission, None), "nocam")
+    assert np.all(got[:, 126:142].view(np.uint32) == 0)
+
+
+def test_special_values(torch_cuda, hip):
+    note("non-finite / signed-zero inputs, 256 envs")
+    b = synth.make_batch(256, seed=99, variant=synth.SPECIAL)
+    got = run_device(torch_cuda, hip, b.obs, b.mission, b.cameras)
+    assert_feature_parity(got, oracle.features(b.obs, b.mission, b.cameras), "special")
+
+
+def test_nondefault_stream(torch_cuda, hip):
+    note("non-default stream")
+    torch = torch_cuda
+    b = synth.make_batch(300, seed=12)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        got = run_device(torch, hip, b.obs, b.mission, b.cameras, stream=s)
+    assert_feature_parity(got, oracle.features(b.obs, b.mission, b.cameras), "stream")
+
+
+def strided_case(torch, hip, batch, record, obs_off, mis_off, cam_off, label):
+    buf = np.zeros(batch * record, np.uint8)
+    synth.fill_records(buf, batch, record, obs_off, mis_off, cam_off, seed=77, threads=16)
+    want = oracle.features_strided(buf, batch, record, obs_off, mis_off, cam_off, threads=16)
+    d = torch.from_numpy(buf).cuda()
+    out = torch.full((batch, 142), float("nan"), dtype=torch.float32, device="cuda")
+    base = d.data_ptr()
+    s = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    assert hip.extract_features_strided_device(base + obs_off, record, base + mis_off, record,
+                                               base + cam_off, record, out, batch, s) == 1
+    assert hip.synchronize(s) == 1
+    got = out.cpu().numpy()
+    del d
+    return assert_feature_parity(got, want, label)
+
+
+@pytest.mark.parametrize("which", ["obs", "next_obs"])
+def test_replay_records_small(torch_cuda, hip, which):
+    note(f"replay records, 512 envs, {which}")
+    offs = (OFF_OBS, OFF_MISSION, OFF_CAM) if which == "obs" else \
+        (OFF_NEXT_OBS, OFF_NEXT_MISSION, OFF_NEXT_CAM)
+    strided_case(torch_cuda, hip, 512, RECORD, *offs, f"replay-{which}")
+
+
+def test_byte_aligned_cameras(torch_cuda, hip):
+    note("strided, byte-aligned camera rows")
+    strided_case(torch_cuda, hip, 257, 33020, 0, 16592, 16633, "byte-aligned")
+
+
+def test_config5_replay_65536(torch_cuda, hip):
+    note("config 5: 65536 records x 66672 B")
+    stats = strided_case(torch_cuda, hip, 65536, RECORD, OFF_OBS, OFF_MISSION, OFF_CAM, "c5")
+    note(f"c5 stats {stats}")
+
+
+def test_lidar_transform_accuracy(torch_cuda, hip):
+    note("per-bin transform over a strided sweep of [0,120] and specials")
+    torch = torch_cuda
+    top = np.float32(120.0).view(np.uint32)
+    bits = np.arange(0, int(top) + 1, 61, dtype=np.uint32)
+    specials = np.array([0.0, -0.0, 1e-45, 1e-38, 1e-30, 1e-8, 0.05, 0.2, 1.0, 2.0, 119.99, 120.0,
+                         120.5, 300.0, 3e38, np.inf, -np.inf, np.nan, -1.0, -1e-30],
+                        np.float32)
+    xs = np.concatenate([bits.view(np.float32), specials])
+    d_in = torch.from_numpy(xs).cuda()
+    d_out = torch.empty_like(d_in)
+    s = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    assert hip.lidar_transform_device(d_in, d_out, xs.size, s) == 1
+    assert hip.synchronize(s) == 1
+    got = d_out.cpu().numpy()
+    want = oracle.lidar_feature(xs)
+    valid = (xs >= 0) & np.isfinite(xs)
+    assert np.all(got[~valid] == -1.0)
+    g, w = got[valid], want[valid]
+    assert np.array_equal(np.signbit(g[w == 0]), np.signbit(w[w == 0]))
+    ulp = np.abs(g.view(np.int32).astype(np.int64) - w.view(np.int32).astype(np.int64))
+    note(f"transform: {valid.sum()} values, max ulp {ulp.max()}, "
+         f"exact {np.mean(ulp == 0):.4f}, <=1ulp {np.mean(ulp <= 1):.6f}")
+    assert ulp.max() <= 4
+
+
+def test_abi_errors_with_device(hip):
+    note("ABI error paths with a device present")
+    assert hip.FeatureBatch.create(4096, 8) is None        # no such device
+    b = hip.FeatureBatch.create(0, 4)
+    assert b is not None
+    try:
+        obs = np.zeros((8, 4148), np.float32)
+        mis = np.zeros((8, 10), np.float32)
+        cam = np.zeros((8, 16384), np.uint8)
+        out = np.zeros((8, 142), np.float32)
+        assert b.extract_host(obs, mis, cam, 0, out) == 0
+        assert b.extract_host(obs, mis, cam, 5, out) == 0     # above max_batch
+        assert b.error() == ""
+        assert b.extract_host(obs, mis, cam, 4, out) == 1
+        assert b.error() == ""
+        assert np.all(out[:4, 62:126] == 0.0) and np.all(out[4:] == 0.0)
+    finally:
+        b.destroy()
+
+
+def test_reference_test_binary_drop_in():
+    """The reference's own tests/test_cuda_features.c + training.c, compiled
+    from the reference sources by oracle/Makefile (droptest) and linked
+    against libturbinator_hip.so."""
+    exe = oracle.HERE / "_ref" / "test_cuda_features_dropin"
+    if not exe.exists():
+        pytest.skip("drop-in binary not built (reference tree absent at build time)")
+    note("reference test_cuda_features.c linked against libturbinator_hip.so")
+    env = dict(os.environ, TB_CUDA_TEST_DEVICE="0")
+    proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120, env=env)
+    note(f"drop-in: rc={proc.returncode} out={proc.stdout.strip()} err={proc.stderr.strip()}")
+    assert proc.returncode == 0
+    assert "matches C11 extraction" in proc.stdout

@@ -1,0 +1,179 @@
+"""Pins the CPU oracle (oracle/features_oracle.c) before it is trusted.
+
+Checks, each chosen so a plausible restatement mistake fails one of them:
+  * bit-for-bit equality with the golden outputs the reference's own
+    src/training/training.c produced (tests/golden/) and, where it is built,
+    with that compiled reference on fresh seeded batches of every variant;
+  * the reference's own assertions (tests/test_training.c:25-35);
+  * closed forms: constant-pixel quadrant = p/255, all-sentinel sector = -1,
+    all-far sector = 1, scale boundaries, NULL cameras, arena mask;
+  * index maps by brute force: perturbing one LiDAR bin or one camera pixel
+    changes exactly the one sector / quadrant the reference layout assigns.
+"""
+from __future__ import annotations
+
+import json
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.golden.make_golden import C4_BATCH, C4_ENVS, envs_inputs, fixture_sets, digest
+from turbinator_c_amd import synth
+
+GOLDEN = np.load(oracle.HERE.parent / "tests" / "golden" / "features_golden.npz")
+GOLDEN_META = json.loads((oracle.HERE.parent / "tests" / "golden" /
+                          "features_golden.json").read_text())
+
+
+@pytest.mark.parametrize("name", ["ref3", "c1", "c4", "special"])
+def test_oracle_matches_reference_golden(name):
+    sets = {n: (inputs, info) for n, inputs, info in fixture_sets()}
+    (obs, mission, cameras), _ = sets[name]
+    assert digest(obs, mission, cameras) == GOLDEN_META["sets"][name]["inputs_sha256"], \
+        "generator no longer reproduces the fixture inputs"
+    got = oracle.features(obs, mission, cameras)
+    want = GOLDEN[name]
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
+def test_oracle_matches_compiled_reference(variant):
+    if oracle.ref_lib() is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    b = synth.make_batch(24, seed=1000 + variant, variant=variant)
+    got = oracle.features(b.obs, b.mission, b.cameras)
+    want = oracle.reference_features(b.obs, b.mission, b.cameras)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    got_nocam = oracle.features(b.obs, b.mission, None)
+    want_nocam = oracle.reference_features(b.obs, b.mission, None)
+    assert np.array_equal(got_nocam.view(np.uint32), want_nocam.view(np.uint32))
+
+
+def test_reference_assertions():
+    """tests/test_training.c:25-35 of the reference."""
+    obs = np.zeros((1, 4148), np.float32)
+    mission = np.zeros((1, 10), np.float32)
+    cams = np.full((1, 16384), 128, np.uint8)
+    mission[0, 0] = 1.0
+    obs[0, 2] = 2.0
+    f = oracle.features(obs, mission, cams)[0]
+    assert f[2] > 0.0 and f[126] > 0.0
+    mission[0, 6] = 1.0
+    mission[0, 7] = 0.9
+    f = oracle.features(obs, mission, cams)[0]
+    assert f[59] == 0.0
+
+
+@pytest.mark.parametrize("p", [0, 1, 37, 128, 207, 254, 255])
+def test_constant_camera_quadrants_are_p_over_255(p):
+    obs = np.zeros((1, 4148), np.float32)
+    mission = np.zeros((1, 10), np.float32)
+    cams = np.full((1, 16384), p, np.uint8)
+    f = oracle.features(obs, mission, cams)[0]
+    want = np.float32(p) / np.float32(255)
+    assert np.all(f[126:142] == want)
+
+
+def test_sentinel_and_far_sectors_are_exact():
+    obs = np.zeros((2, 4148), np.float32)
+    mission = np.zeros((2, 10), np.float32)
+    obs[0, 48:4144] = -1.0
+    obs[1, 48:4144] = np.float32(250.0)
+    f = oracle.features(obs, mission, None)
+    assert np.all(f[0, 62:126] == -1.0)
+    assert np.all(f[1, 62:126] == 1.0)
+    assert np.all(f[:, 126:142] == 0.0)
+
+
+def test_scalar_scale_boundaries_and_clamps():
+    pi = np.float32(3.14159265358979323846)
+    scales = np.ones(48, np.float32)
+    scales[0:2] = 300
+    scales[2] = 100
+    scales[3:6] = 50
+    scales[10:13] = 5
+    scales[13:16] = 30
+    scales[28:32] = pi / np.float32(4)
+    scales[32:40] = 5
+    scales[44:46] = pi / np.float32(2)
+    obs = np.zeros((3, 4148), np.float32)
+    mission = np.zeros((3, 10), np.float32)
+    obs[0, :48] = scales
+    obs[1, :48] = -scales
+    obs[2, :48] = scales * np.float32(0.5)
+    obs[0, 4144:4148] = [2.0, -1.0, 0.25, np.inf]
+    f = oracle.features(obs, mission, None)
+    assert np.all(f[0, :48] == 1.0) and np.all(f[1, :48] == -1.0)
+    assert np.all(f[2, :48] == np.float32(0.5))
+    assert list(f[0, 48:52]) == [1.0, 0.0, 0.25, 0.0]
+
+
+def test_arena_mask_threshold_is_strict():
+    obs = np.zeros((3, 4148), np.float32)
+    mission = np.full((3, 10), np.float32(0.75), np.float32)
+    mission[:, 6] = [0.5, np.nextafter(np.float32(0.5), np.float32(1)), np.inf]
+    f = oracle.features(obs, mission, None)
+    assert np.all(f[0, 59:62] == np.float32(0.75))   # 0.5 is not > 0.5
+    assert np.all(f[1, 59:62] == 0.0)                # just above masks
+    assert np.all(f[2, 59:62] == np.float32(0.75))   # +inf -> 0 before compare
+    assert f[2, 58] == 0.0                           # non-finite m[6] itself -> 0
+
+
+def test_lidar_index_map_by_perturbation():
+    base = np.zeros((1, 4148), np.float32)
+    base[0, 48:4144] = 300.0
+    mission = np.zeros((1, 10), np.float32)
+    f0 = oracle.features(base, mission, None)[0]
+    rng = np.random.default_rng(3)
+    for b in rng.choice(4096, 64, replace=False):
+        o = base.copy()
+        o[0, 48 + b] = -1.0
+        f = oracle.features(o, mission, None)[0]
+        changed = np.nonzero(f != f0)[0]
+        head, row, az = b // 2048, (b % 2048) // 128, b % 128
+        want = 62 + head * 32 + (row // 4) * 8 + az // 16
+        assert list(changed) == [want], (b, changed)
+
+
+def test_camera_index_map_by_perturbation():
+    cams = np.zeros((1, 16384), np.uint8)
+    obs = np.zeros((1, 4148), np.float32)
+    mission = np.zeros((1, 10), np.float32)
+    rng = np.random.default_rng(4)
+    for p in rng.choice(16384, 64, replace=False):
+        c = cams.copy()
+        c[0, p] = 255
+        f = oracle.features(obs, mission, c)[0]
+        changed = np.nonzero(f[126:] != 0)[0]
+        cam, y, x = p // 4096, (p % 4096) // 64, p % 64
+        assert list(changed) == [cam * 4 + (y // 32) * 2 + x // 32]
+        assert f[126 + changed[0]] == np.float32(255) / np.float32(261120)
+
+
+def test_lidar_transform_is_log1p_ratio():
+    """f(r) = log1p(min(r,120))/log1p(120) within 1 ulp of the double form;
+    distinguishes log1p from log, the 120 m clamp and the sentinel rule."""
+    xs = np.array([0.0, 1e-30, 1e-8, 0.05, 0.2, 0.5, 1.0, np.e - 1, 37.5, 119.99, 120.0, 121.0,
+                   300.0], np.float32)
+    got = oracle.lidar_feature(xs)
+    want = np.log1p(np.minimum(xs.astype(np.float64), 120.0)) / math.log1p(120.0)
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 1.5 * ulp)
+    assert np.all(oracle.lidar_feature(np.array([-1.0, -1e-30, np.nan, np.inf, -np.inf],
+                                                np.float32)) == -1.0)
+    assert oracle.lidar_feature(np.array([-0.0], np.float32))[0] == 0.0
+
+
+def test_batch_threads_are_invariant():
+    b = synth.make_batch(64, seed=9)
+    one = oracle.features(b.obs, b.mission, b.cameras, threads=1)
+    many = oracle.features(b.obs, b.mission, b.cameras, threads=7)
+    assert np.array_equal(one.view(np.uint32), many.view(np.uint32))
+
+
+def test_golden_c4_covers_every_quarter():
+    assert sorted({1 + e * 4 // C4_BATCH for e in C4_ENVS}) == [1, 2, 3, 4]
+    obs, mission, cams = envs_inputs(42, C4_ENVS[:4], [1] * 4)
+    assert np.all(obs[:, 48:4144] == -1.0)

@@ -1,0 +1,103 @@
+"""Builds the gfx950 feature library and the host helpers in-tree.
+
+Outputs (git-ignored, shipped with the working tree):
+  turbinator_c_amd/libturbinator_hip.so    HIP kernels + the C-ABI boundary
+  turbinator_c_amd/libturbinator_synth.so  seeded synthetic batch generator
+  oracle/liboracle.so, oracle/_ref/...     CPU checker (test infrastructure)
+
+Run as ``python -m turbinator_c_amd.build``.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+INCLUDE = ROOT / "include"
+BUILD = ROOT / "_build"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+
+ARCH = "gfx950"
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    f"-I{INCLUDE}",
+]
+C_FLAGS = ["-O2", "-std=c11", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
+           f"-I{ROCM / 'include'}", f"-I{INCLUDE}"]
+
+HIP_SOURCES = ["features.hip"]
+HOST_C_SOURCES = ["feature_batch.c"]
+
+LIB_HIP = PKG / "libturbinator_hip.so"
+LIB_SYNTH = PKG / "libturbinator_synth.so"
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in proc.stdout.splitlines()
+                    if "packed-fp32-ops' is not a recognized feature" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out)
+
+
+def hipcc() -> str:
+    exe = shutil.which("hipcc") or str(ROCM / "bin" / "hipcc")
+    if not Path(exe).exists():
+        raise RuntimeError("hipcc not found; the gfx950 library cannot be built")
+    return exe
+
+
+def build_hip_library() -> Path:
+    BUILD.mkdir(exist_ok=True)
+    objs = []
+    for src in HIP_SOURCES:
+        obj = BUILD / (Path(src).stem + ".hip.o")
+        _run([hipcc(), *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        objs.append(obj)
+    for src in HOST_C_SOURCES:
+        obj = BUILD / (Path(src).stem + ".c.o")
+        _run(["gcc", *C_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        objs.append(obj)
+    tmp = LIB_HIP.with_suffix(".so.tmp")
+    _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+          *map(str, objs), f"-L{ROCM / 'lib'}", "-lamdhip64",
+          f"-Wl,-rpath,{ROCM / 'lib'}"])
+    os.replace(tmp, LIB_HIP)
+    return LIB_HIP
+
+
+def build_synth_library() -> Path:
+    tmp = LIB_SYNTH.with_suffix(".so.tmp")
+    _run(["gcc", "-O3", "-std=c11", "-fPIC", "-shared", "-Wall", "-Wextra",
+          "-D_POSIX_C_SOURCE=200809L", "-o", str(tmp), str(CSRC / "synth.c"), "-lm", "-lpthread"])
+    os.replace(tmp, LIB_SYNTH)
+    return LIB_SYNTH
+
+
+def build_oracle() -> None:
+    _run(["make", "-s", "-C", str(ROOT / "oracle"), "all"])
+
+
+def build_all() -> None:
+    build_synth_library()
+    build_oracle()
+    build_hip_library()
+
+
+if __name__ == "__main__":
+    build_all()
+    print("built", LIB_HIP, LIB_SYNTH, file=sys.stderr)

@@ -1,0 +1,107 @@
+"""Python mirror of the sensor-feature boundary (include/turbinator/training/).
+
+Names, argument meaning and return codes follow the reference C interface
+include/turbinator/training/cuda_features.h:14-34 (src/cuda/features.cu):
+functions return 1 on success and 0 on failure, exactly like the C entry
+points they call.  Device arguments accept torch tensors on the GPU or raw
+integer device addresses; `stream` accepts a torch.cuda.Stream, a raw
+hipStream_t integer or None (null stream).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .native import CAMERA_BYTES, FEATURE_DIM, MISSION_DIM, OBS_DIM, hip_lib
+
+
+def _dev(x) -> int | None:
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def _stream(s) -> int | None:
+    if s is None:
+        return None
+    if isinstance(s, int):
+        return s
+    return s.cuda_stream
+
+
+def extract_features_device(obs, mission, cameras, features, batch_size: int,
+                            stream=None) -> int:
+    """tb_cuda_extract_features_device (cuda_features.h:14-19)."""
+    return hip_lib().tb_cuda_extract_features_device(
+        _dev(obs), _dev(mission), _dev(cameras), _dev(features), batch_size, _stream(stream))
+
+
+def extract_features_strided_device(obs, obs_stride: int, mission, mission_stride: int,
+                                    cameras, camera_stride: int, features, batch_size: int,
+                                    stream=None) -> int:
+    """tb_hip_extract_features_strided_device (hip_features.h)."""
+    return hip_lib().tb_hip_extract_features_strided_device(
+        _dev(obs), obs_stride, _dev(mission), mission_stride, _dev(cameras), camera_stride,
+        _dev(features), batch_size, _stream(stream))
+
+
+def lidar_transform_device(ranges, out, count: int, stream=None) -> int:
+    """tb_hip_lidar_transform_device (hip_features.h)."""
+    return hip_lib().tb_hip_lidar_transform_device(_dev(ranges), _dev(out), count,
+                                                   _stream(stream))
+
+
+def synchronize(stream=None) -> int:
+    """tb_cuda_synchronize (cuda_features.h:20)."""
+    return hip_lib().tb_cuda_synchronize(_stream(stream))
+
+
+class FeatureBatch:
+    """tb_cuda_feature_batch handle (cuda_features.h:22-34)."""
+
+    def __init__(self, handle: int):
+        self._handle = handle
+
+    @classmethod
+    def create(cls, device_id: int, max_batch: int) -> "FeatureBatch | None":
+        h = hip_lib().tb_cuda_feature_batch_create(device_id, max_batch)
+        return cls(h) if h else None
+
+    @property
+    def handle(self) -> int | None:
+        return self._handle
+
+    def error(self) -> str:
+        return hip_lib().tb_cuda_feature_batch_error(self._handle).decode()
+
+    def extract_host(self, obs: np.ndarray, mission: np.ndarray, cameras: np.ndarray,
+                     count: int, out: np.ndarray) -> int:
+        for a, dt, width in ((obs, np.float32, OBS_DIM), (mission, np.float32, MISSION_DIM),
+                             (cameras, np.uint8, CAMERA_BYTES), (out, np.float32, FEATURE_DIM)):
+            if a.dtype != dt or not a.flags.c_contiguous or a.size < count * width:
+                raise ValueError("host arrays must be C-contiguous with count rows of the "
+                                 "reference layout")
+        return hip_lib().tb_cuda_extract_features_host(
+            self._handle, obs.ctypes.data, mission.ctypes.data, cameras.ctypes.data, count,
+            out.ctypes.data)
+
+    def destroy(self) -> None:
+        if self._handle:
+            hip_lib().tb_cuda_feature_batch_destroy(self._handle)
+            self._handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.destroy()
+
+
+def feature_batch_error(handle) -> str:
+    """tb_cuda_feature_batch_error for a raw handle (None -> NULL)."""
+    return hip_lib().tb_cuda_feature_batch_error(handle).decode()
+
+
+__all__ = ["extract_features_device", "extract_features_strided_device",
+           "lidar_transform_device", "synchronize", "FeatureBatch", "feature_batch_error"]
