@@ -155,6 +155,11 @@ def test_replay_records_small(torch_cuda, hip, which):
     strided_case(torch_cuda, hip, 512, RECORD, *offs, f"replay-{which}")
 
 
+def test_eight_byte_aligned_rows(torch_cuda, hip):
+    note("strided, 8-byte aligned obs and camera rows")
+    strided_case(torch_cuda, hip, 300, 33032, 0, 16600, 16640, "eight-byte")
+
+
 def test_byte_aligned_cameras(torch_cuda, hip):
     note("strided, byte-aligned camera rows")
     strided_case(torch_cuda, hip, 257, 33020, 0, 16592, 16633, "byte-aligned")

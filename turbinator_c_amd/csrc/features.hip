@@ -2,18 +2,25 @@
 //
 // Semantics follow the reference CPU twin tb_train_extract_features_cpu
 // (src/training/training.c:57-142); the reference CUDA kernel it replaces is
-// src/cuda/features.cu:90-169.  Design (HBM-bound streaming reduction, no
-// MFMA):
-//   * one wavefront (64 lanes) per environment, four environments per
-//     256-thread workgroup, grid-stride over environments;
-//   * lane s owns LiDAR sector s (head = s/32, elevation sector = (s/8)%4,
-//     azimuth sector = s%8) and reads its four 64-byte row runs with 128-bit
-//     loads, summing the 64 bins in the reference order (row outer, bin
-//     inner), so the only difference from the CPU is the per-bin log1p;
-//   * cameras stream as 16 fully coalesced 1 KiB wave loads per environment;
-//     byte sums use v_dot4_u32_u8 and a cross-lane integer reduction, so the
-//     16 quadrant means are bit-exact;
-//   * lanes 0..61 produce the clamp and mission features (bit-exact).
+// src/cuda/features.cu:90-169.  The path is an HBM-bound streaming reduction
+// (33,584 algorithmic bytes and ~4,100 log evaluations per environment), so
+// the design is about coalescing and bytes in flight, not MFMA:
+//
+//   * one 256-thread workgroup (4 wave64) per environment, grid-stride over
+//     environments; each wave issues 8 fully coalesced 1 KiB loads (4 LiDAR,
+//     4 camera), so a workgroup holds the environment's 32 KiB in flight;
+//   * wave w reads LiDAR floats [1024w, 1024w+1024) as float4 per lane,
+//     evaluates the bin transform in registers and writes the values into an
+//     LDS stage laid out sector-major: chunk c (row el = c/4, bins 4(c%4)..+3)
+//     of sector s at 16-byte unit c*68 + s.  The pitch of 68 units makes the
+//     stage writes conflict-free over 64 banks and the reads (lane s walks
+//     c = 0..15) conflict-free on any bank count;
+//   * after one barrier wave 0 sums its sector's 64 values sequentially in
+//     the reference order (row outer, bin inner), so the LiDAR means differ
+//     from the CPU only by the per-bin log1p, never by summation order;
+//   * wave w also owns camera w: v_dot4_u32_u8 byte sums and a cross-lane
+//     integer reduction make the 16 quadrant means bit-exact;
+//   * wave 1 produces the 62 clamp and mission features (bit-exact).
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -27,22 +34,21 @@ namespace {
 constexpr int kObsDim = 4148;
 constexpr int kFeatureDim = 142;
 constexpr int kLidarOffset = 48;
-constexpr int kWave = 64;
-constexpr int kEnvsPerBlock = 4;
-constexpr int kBlockThreads = kWave * kEnvsPerBlock;
+constexpr int kBlockThreads = 256;
+constexpr int kStagePitch = 68;  // 16-byte units per LDS stage chunk row
 constexpr unsigned kMaxBlocks = 1u << 20;
 constexpr size_t kMaxBatch = 0x7fffffffu;
 
-// log1pf(120.0f) as the reference evaluates it (glibc and GCC's folding
-// agree; it is the correctly rounded float of ln 121).
-constexpr float kLog1p120 = 0x1.32ee3cp+2f;
-// ln2 / kLog1p120 split into two floats, and 1 / kLog1p120.
+// L = log1pf(120.0f) = 0x1.32ee3cp+2 as the reference evaluates it (glibc
+// and GCC's constant folding agree; it is the correctly rounded float of
+// ln 121).  ln2 / L split into two floats, and 1 / L:
 constexpr float kLn2OverLHi = 0x1.28009cp-3f;
 constexpr float kLn2OverLLo = -0x1.9578d6p-29f;
 constexpr float kInvL = 0x1.ab0a8ap-3f;
 constexpr float kPi = 3.14159265358979323846f;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
@@ -97,8 +103,24 @@ __device__ __forceinline__ float scalar_scale(int i) {  // training.c:70-81
     return s;
 }
 
+// Four consecutive floats; LV is the widest load the row alignment allows.
+template <int LV>
+__device__ __forceinline__ f32x4 load_lidar4(const float *p) {
+    if constexpr (LV == 4) {
+        return __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+    } else if constexpr (LV == 2) {
+        const f32x2 lo = __builtin_nontemporal_load(reinterpret_cast<const f32x2 *>(p));
+        const f32x2 hi = __builtin_nontemporal_load(reinterpret_cast<const f32x2 *>(p + 2));
+        return f32x4{lo.x, lo.y, hi.x, hi.y};
+    } else {
+        return f32x4{__builtin_nontemporal_load(p), __builtin_nontemporal_load(p + 1),
+                     __builtin_nontemporal_load(p + 2), __builtin_nontemporal_load(p + 3)};
+    }
+}
+
+// Sixteen consecutive camera bytes; CV is the widest load the alignment allows.
 template <int CV>
-__device__ __forceinline__ u32x4 load_camera_chunk(const unsigned char *p) {
+__device__ __forceinline__ u32x4 load_camera16(const unsigned char *p) {
     if constexpr (CV == 16) {
         return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
     } else if constexpr (CV == 8) {
@@ -107,7 +129,8 @@ __device__ __forceinline__ u32x4 load_camera_chunk(const unsigned char *p) {
         return u32x4{lo.x, lo.y, hi.x, hi.y};
     } else if constexpr (CV == 4) {
         const unsigned *q = reinterpret_cast<const unsigned *>(p);
-        return u32x4{q[0], q[1], q[2], q[3]};
+        return u32x4{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1),
+                     __builtin_nontemporal_load(q + 2), __builtin_nontemporal_load(q + 3)};
     } else {
         unsigned w[4];
         for (int k = 0; k < 4; ++k)
@@ -124,108 +147,109 @@ __device__ __forceinline__ unsigned byte_sum(u32x4 w, unsigned acc) {
     return __builtin_amdgcn_udot4(w.w, 0x01010101u, acc, false);
 }
 
-// LV: floats per LiDAR load (4 when every row run is 16-byte aligned, else 1).
-// CV: bytes per camera load unit (16, 8, 4 or 1, from the row alignment).
+// Sum over the 32 lanes that share lane bit 1 (the camera column half qx).
+__device__ __forceinline__ unsigned sum_same_qx(unsigned v) {
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 4);
+    v += __shfl_xor(v, 8);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+// LV: floats per LiDAR load (4, 2 or 1 from the row alignment).
+// CV: bytes per camera load (16, 8, 4 or 1 from the row alignment).
 template <int LV, int CV>
 __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const unsigned wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const size_t first = (size_t)blockIdx.x * kEnvsPerBlock + wave;
-    const size_t step = (size_t)gridDim.x * kEnvsPerBlock;
+    __shared__ f32x4 stage[16 * kStagePitch];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool has_cameras = rows.cameras != nullptr;
 
-    // LiDAR sector of this lane.
-    const int head = lane >> 5, es = (lane >> 3) & 3, as = lane & 7;
-    const int sector_off = kLidarOffset + head * 2048 + es * 512 + as * 16;
+    // Stage position of this lane's float4 for each of the wave's 4 loads:
+    // LiDAR float4 index i*64 + lane (i = 4w + k) is row (i%8)*2 + lane/32
+    // of head i/8, azimuth sector (lane%32)/4, bins 4*(lane%4)..+3.
+    int unit[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int i = 4 * w + k, head = i >> 3, row = ((i & 7) << 1) + (lane >> 5);
+        const int sector = head * 32 + (row >> 2) * 8 + ((lane & 31) >> 2);
+        const int chunk = (row & 3) * 4 + (lane & 3);
+        unit[k] = chunk * kStagePitch + sector;
+    }
 
-    for (size_t env = first; env < rows.batch; env += step) {
+    for (size_t env = blockIdx.x; env < rows.batch; env += gridDim.x) {
         const float *obs = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
-        const float *mission =
-            reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride);
+        const float *lidar = obs + kLidarOffset;
         float *out = rows.out + env * kFeatureDim;
 
-        // ---- LiDAR sector sum, reference order: row el outer, bin az inner.
-        const float *sec = obs + sector_off;
-        float sum = 0.0f;
-        if constexpr (LV == 4) {
-            f32x4 v[16];
+        // Issue every load of this wave before using any of them.
+        f32x4 v[4];
+        u32x4 px[4];
 #pragma unroll
-            for (int el = 0; el < 4; ++el)
+        for (int k = 0; k < 4; ++k) v[k] = load_lidar4<LV>(lidar + (4 * w + k) * 256 + 4 * lane);
+        if (has_cameras) {
+            // Camera w, rows 16k + lane/4, bytes 16*(lane%4)..+15.
+            const unsigned char *cam = rows.cameras + env * rows.camera_stride + w * 4096;
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    v[el * 4 + j] = __builtin_nontemporal_load(
-                        reinterpret_cast<const f32x4 *>(sec + el * 128 + 4 * j));
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                sum += lidar_bin_feature(v[k].x);
-                sum += lidar_bin_feature(v[k].y);
-                sum += lidar_bin_feature(v[k].z);
-                sum += lidar_bin_feature(v[k].w);
-            }
-        } else {
-#pragma unroll
-            for (int el = 0; el < 4; ++el) {
-                float v[16];
-#pragma unroll
-                for (int az = 0; az < 16; ++az) v[az] = sec[el * 128 + az];
-#pragma unroll
-                for (int az = 0; az < 16; ++az) sum += lidar_bin_feature(v[az]);
-            }
+            for (int k = 0; k < 4; ++k) px[k] = load_camera16<CV>(cam + (k * 64 + lane) * 16);
         }
 
-        // ---- Camera quadrant byte sums.  Chunk k = it*64 + lane of the
-        // environment's 1024 16-byte chunks lies in camera it/4, row
-        // (it%4)*16 + lane/4, columns 16*(lane%4)..+15, i.e. quadrant
-        // (cam = it/4, qy = (it%4)/2, qx = (lane>>1)&1); accumulator it/2.
-        float cam_mean = 0.0f;
-        if (rows.cameras) {
-            const unsigned char *cam = rows.cameras + env * rows.camera_stride;
-            unsigned acc[8];
 #pragma unroll
-            for (int a = 0; a < 8; ++a) acc[a] = 0u;
-#pragma unroll
-            for (int it = 0; it < 16; ++it) {
-                const u32x4 w = load_camera_chunk<CV>(cam + (size_t)(it * 64 + lane) * 16);
-                acc[it >> 1] = byte_sum(w, acc[it >> 1]);
-            }
-            // Sum over the 32 lanes sharing qx (lane bit 1 untouched).
-#pragma unroll
-            for (int a = 0; a < 8; ++a) {
-                unsigned v = acc[a];
-                v += __shfl_xor(v, 1);
-                v += __shfl_xor(v, 4);
-                v += __shfl_xor(v, 8);
-                v += __shfl_xor(v, 16);
-                v += __shfl_xor(v, 32);
-                acc[a] = v;
-            }
-            // Output lane q < 16 wants accumulator q/2 of qx = q&1, held by
-            // lane 2*(q&1).
-            const int src = (lane & 1) << 1;
-            unsigned pick = 0u;
-#pragma unroll
-            for (int a = 0; a < 8; ++a) {
-                const unsigned v = __shfl(acc[a], src);
-                pick = ((lane >> 1) == a) ? v : pick;
-            }
-            cam_mean = (float)pick / (1024.0f * 255.0f);  // training.c:138
+        for (int k = 0; k < 4; ++k) {
+            f32x4 f;
+            f.x = lidar_bin_feature(v[k].x);
+            f.y = lidar_bin_feature(v[k].y);
+            f.z = lidar_bin_feature(v[k].z);
+            f.w = lidar_bin_feature(v[k].w);
+            stage[unit[k]] = f;
         }
 
-        // ---- Proprioception, scan statistics and mission (training.c:107-112).
-        float scalar = 0.0f;
-        if (lane < 48) {
-            scalar = clamp_ref(finite_or_zero(obs[lane]) / scalar_scale(lane), -1.0f, 1.0f);
-        } else if (lane < 52) {
-            scalar = clamp_ref(finite_or_zero(obs[4144 + lane - 48]), 0.0f, 1.0f);
-        } else if (lane < 62) {
-            const int i = lane - 52;
-            const bool arena = finite_or_zero(mission[6]) > 0.5f;
-            const float v = (i >= 7 && arena) ? 0.0f : mission[i];
-            scalar = clamp_ref(finite_or_zero(v), -1.0f, 1.0f);
+        // Quadrant (cam w, qy, qx = lane bit 1): loads k = 0,1 cover rows
+        // 0..31 (qy 0), k = 2,3 rows 32..63 (qy 1).  training.c:128-141.
+        if (has_cameras) {
+            const unsigned top = sum_same_qx(byte_sum(px[1], byte_sum(px[0], 0u)));
+            const unsigned bottom = sum_same_qx(byte_sum(px[3], byte_sum(px[2], 0u)));
+            if (lane == 0 || lane == 2) {
+                const int qx = lane >> 1;
+                out[126 + w * 4 + qx] = (float)top / (1024.0f * 255.0f);
+                out[126 + w * 4 + 2 + qx] = (float)bottom / (1024.0f * 255.0f);
+            }
+        } else if (lane < 4) {
+            out[126 + w * 4 + lane] = 0.0f;
         }
 
-        if (lane < 62) out[lane] = scalar;
-        out[62 + lane] = sum / 64.0f;
-        if (lane < 16) out[126 + lane] = cam_mean;
+        __syncthreads();
+        if (w == 0) {
+            // training.c:113-127: sequential sum, row outer, bin inner.
+            float sum = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                const f32x4 f = stage[c * kStagePitch + lane];
+                sum += f.x;
+                sum += f.y;
+                sum += f.z;
+                sum += f.w;
+            }
+            out[62 + lane] = sum / 64.0f;
+        } else if (w == 1 && lane < 62) {
+            // training.c:107-112.
+            float scalar;
+            if (lane < 48) {
+                scalar = clamp_ref(finite_or_zero(obs[lane]) / scalar_scale(lane), -1.0f, 1.0f);
+            } else if (lane < 52) {
+                scalar = clamp_ref(finite_or_zero(obs[4144 + lane - 48]), 0.0f, 1.0f);
+            } else {
+                const float *mission =
+                    reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride);
+                const int i = lane - 52;
+                const bool arena = finite_or_zero(mission[6]) > 0.5f;
+                const float m = (i >= 7 && arena) ? 0.0f : mission[i];
+                scalar = clamp_ref(finite_or_zero(m), -1.0f, 1.0f);
+            }
+            out[lane] = scalar;
+        }
+        __syncthreads();  // the stage is reused by the next environment
     }
 }
 
@@ -236,11 +260,10 @@ __global__ __launch_bounds__(256) void lidar_transform_kernel(const float *in, f
         out[i] = lidar_bin_feature(in[i]);
 }
 
-int camera_vector_bytes(const void *cameras, size_t stride) {
-    const uintptr_t bits = reinterpret_cast<uintptr_t>(cameras) | (uintptr_t)stride;
-    if ((bits & 15u) == 0) return 16;
-    if ((bits & 7u) == 0) return 8;
-    if ((bits & 3u) == 0) return 4;
+int vector_bytes(const void *base, size_t stride, int widest) {
+    const uintptr_t bits = reinterpret_cast<uintptr_t>(base) | (uintptr_t)stride;
+    for (int v = widest; v > 1; v >>= 1)
+        if ((bits & (uintptr_t)(v - 1)) == 0) return v;
     return 1;
 }
 
@@ -255,14 +278,17 @@ void launch_lv(const Rows &rows, int cv, unsigned blocks, hipStream_t stream) {
 }
 
 int launch_features(const Rows &rows, hipStream_t stream) {
-    const uintptr_t lidar_bits =
-        (reinterpret_cast<uintptr_t>(rows.obs) + kLidarOffset * sizeof(float)) |
-        (uintptr_t)rows.obs_stride;
-    const int lv = (lidar_bits & 15u) == 0 ? 4 : 1;
-    const int cv = rows.cameras ? camera_vector_bytes(rows.cameras, rows.camera_stride) : 16;
-    size_t want = (rows.batch + kEnvsPerBlock - 1) / kEnvsPerBlock;
-    const unsigned blocks = want > kMaxBlocks ? kMaxBlocks : (unsigned)want;
+    // Float rows are 4-byte aligned (checked by the callers); the LiDAR block
+    // starts 192 bytes into the row.
+    const int lv = vector_bytes(rows.obs + kLidarOffset * sizeof(float), rows.obs_stride, 16) / 4;
+    const int cv = rows.cameras ? vector_bytes(rows.cameras, rows.camera_stride, 16) : 16;
+    const unsigned blocks = rows.batch > kMaxBlocks ? kMaxBlocks : (unsigned)rows.batch;
+    // Report errors of this launch only: a failure left on the thread by an
+    // unrelated earlier runtime call (e.g. selecting a missing device) is
+    // not a launch failure.
+    (void)hipGetLastError();
     if (lv == 4) launch_lv<4>(rows, cv, blocks, stream);
+    else if (lv == 2) launch_lv<2>(rows, cv, blocks, stream);
     else launch_lv<1>(rows, cv, blocks, stream);
     return hipGetLastError() == hipSuccess;
 }
@@ -317,6 +343,7 @@ extern "C" int tb_hip_lidar_transform_device(const float *ranges, float *out, si
     if (!ranges || !out || count == 0) return 0;
     size_t want = (count + 255) / 256;
     const unsigned blocks = want > kMaxBlocks ? kMaxBlocks : (unsigned)want;
+    (void)hipGetLastError();
     lidar_transform_kernel<<<blocks, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(ranges, out,
                                                                                       count);
     return hipGetLastError() == hipSuccess;
