@@ -87,6 +87,51 @@ def time_gpu(torch, sets, steps: int, warmup: int):
     return start.elapsed_time(stop) / 1e3, wall
 
 
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration(torch, reps: int = 5) -> None:
+    """Device-to-device copies of exactly COPY_BYTES: under rocprofv3 --pmc
+    their FETCH_SIZE / WRITE_SIZE per dispatch calibrate the counters."""
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str) -> dict:
+    """HBM bytes per feature-kernel launch from two rocprofv3 --pmc runs of
+    `bench.py --no-cpu --copy-calibration` (FETCH_SIZE, then WRITE_SIZE; KiB
+    per dispatch), each scaled by what the counter reads for the 1 GiB copy."""
+    import csv
+    import statistics
+
+    def per_kernel(path):
+        out = {}
+        for r in csv.DictReader(open(path)):
+            out.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return out
+
+    f, w = per_kernel(fetch_csv), per_kernel(write_csv)
+    feat = next(k for k in f if "features_kernel" in k)
+    copy = max((k for k in f if "copyBuffer" in k), key=lambda k: statistics.mean(f[k]))
+    copy_kib = COPY_BYTES / 1024
+    f_scale = copy_kib / max(f[copy])
+    w_scale = copy_kib / max(w[copy])
+    fetch_b = statistics.mean(f[feat]) * 1024 * f_scale
+    write_b = statistics.mean(w[feat]) * 1024 * w_scale
+    return {"kernel": feat, "dispatches": len(f[feat]),
+            "fetch_kib_raw": statistics.mean(f[feat]), "write_kib_raw": statistics.mean(w[feat]),
+            "fetch_scale": f_scale, "write_scale": w_scale,
+            "copy_fetch_kib_raw": max(f[copy]), "copy_write_kib_raw": max(w[copy]),
+            "hbm_bytes_per_launch": round(fetch_b + write_b),
+            "algorithmic_bytes_per_launch": BYTES_PER_ENV * BATCH,
+            "traffic_over_algorithmic": (fetch_b + write_b) / (BYTES_PER_ENV * BATCH)}
+
+
 def verify_sample(torch, sets, host0) -> dict:
     """Checks the benchmarked set-0 outputs on 256 envs against the oracle."""
     import oracle
@@ -138,7 +183,16 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=3, help="rotating input buffer sets")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after timing, run 1 GiB device copies (PMC calibration)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write the traffic summary from two rocprofv3 --pmc CSVs and exit")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        summary = summarize_pmc(*args.summarize_pmc)
+        TRAFFIC_FILE.write_text(json.dumps(summary, indent=1) + "\n")
+        print(json.dumps(summary, indent=1))
+        return 0
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the feature path needs no "
               "inter-GPU exchange; see DESIGN.md for how it shards). Use --gpus 1.",
@@ -158,6 +212,8 @@ def main() -> int:
     per_call = gpu_s / args.steps
     stats = verify_sample(torch, sets, host0)
     log(f"[bench] parity sample ok: {stats}")
+    if args.copy_calibration:
+        copy_calibration(torch)
     bytes_per_call = BYTES_PER_ENV * BATCH
     achieved = bytes_per_call / per_call / 1e9
     traffic = None

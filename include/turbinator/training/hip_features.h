@@ -48,6 +48,21 @@ int tb_hip_extract_features_strided_device(const void *obs, size_t obs_stride,
 int tb_hip_lidar_transform_device(const float *ranges, float *out,
                                   size_t count, void *stream);
 
+/* Onboard tactical (24) and physics-prior (15) features of the reference
+ * device function tb_onboard_tactical_prior
+ * (src/network/onboard_features.cuh:515-519), which has no C entry in the
+ * reference: it runs inside the actor input kernel
+ * (src/network/network_gpu.cu:274-304).  Device pointers: obs [batch,4148],
+ * mission [batch,10] -> tactical [batch,24], prior [batch,15].  `diag`
+ * (nullable, [batch,4]) receives the LiDAR scan results the prior uses:
+ * closest in-window return of elevations 0..3, its ray index
+ * head*768 + el*128 + azi (-1 if none, as float), the corridor minimum and
+ * the cluster count (as float).  Returns 0 for NULL obs/mission/tactical/
+ * prior or batch 0 / above 0x7fffffff. */
+int tb_hip_onboard_tactical_prior_device(const float *obs, const float *mission,
+                                         float *tactical, float *prior, float *diag,
+                                         size_t batch_size, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,9 +42,10 @@ def lib() -> ctypes.CDLL:
         l.orc_depth_to_luma.restype = ctypes.c_uint8
         l.orc_diagnostics_env.argtypes = [c_void_p, c_void_p, c_void_p]
         l.orc_diagnostics_env.restype = None
-        if hasattr(l, "orc_onboard_env"):
-            l.orc_onboard_env.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
-            l.orc_onboard_env.restype = None
+        l.orc_onboard_env.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
+        l.orc_onboard_env.restype = None
+        l.orc_onboard_ray_dir.argtypes = [c_int, c_void_p]
+        l.orc_onboard_ray_dir.restype = None
         _orc = l
     return _orc
 
@@ -108,6 +109,26 @@ def lidar_feature(values: np.ndarray, threads: int = 8) -> np.ndarray:
     v = np.ascontiguousarray(values, np.float32)
     out = np.empty_like(v)
     lib().orc_lidar_feature_array(_p(v), _p(out), v.size, threads)
+    return out
+
+
+def onboard(obs: np.ndarray, mission: np.ndarray):
+    """(tactical [B,24], prior [B,15], diag [B,4]) per environment."""
+    b = obs.shape[0]
+    tac = np.empty((b, 24), np.float32)
+    pri = np.empty((b, 15), np.float32)
+    diag = np.empty((b, 4), np.float32)
+    for e in range(b):
+        lib().orc_onboard_env(np.ascontiguousarray(obs[e], np.float32).ctypes.data,
+                              np.ascontiguousarray(mission[e], np.float32).ctypes.data,
+                              tac[e].ctypes.data, pri[e].ctypes.data, diag[e].ctypes.data)
+    return tac, pri, diag
+
+
+def onboard_ray_table() -> np.ndarray:
+    out = np.empty((1536, 3), np.float32)
+    for ray in range(1536):
+        lib().orc_onboard_ray_dir(ray, out[ray].ctypes.data)
     return out
 
 

@@ -118,16 +118,27 @@ typedef struct {
     int cluster_count;
 } ob_scan;
 
-static void ob_ray_world(const float r[9], int head, int el, int azi,
-                         float *rwx, float *rwy, float *rwz) {
+/* Body-frame unit vector of ray (head, el, azi), onboard_features.cuh:194-197. */
+static void ob_ray_dir(int head, int el, int azi, float d[3]) {
     const float pi = OB_PI;
     const float elev = (head == 0 ? 1.0f : -1.0f) * (pi * el / 30.0f);
     const float azim = pi * (0.25f + azi / 64.0f);
-    const float rx = cosf(elev) * cosf(azim), ry = cosf(elev) * sinf(azim);
-    const float rz = sinf(elev);
-    *rwx = r[0] * rx + r[1] * ry + r[2] * rz;
-    *rwy = r[3] * rx + r[4] * ry + r[5] * rz;
-    *rwz = r[6] * rx + r[7] * ry + r[8] * rz;
+    d[0] = cosf(elev) * cosf(azim);
+    d[1] = cosf(elev) * sinf(azim);
+    d[2] = sinf(elev);
+}
+
+void orc_onboard_ray_dir(int ray, float *xyz) {
+    ob_ray_dir(ray / 768, (ray % 768) / 128, ray % 128, xyz);
+}
+
+static void ob_ray_world(const float r[9], int head, int el, int azi,
+                         float *rwx, float *rwy, float *rwz) {
+    float d[3];
+    ob_ray_dir(head, el, azi, d);
+    *rwx = r[0] * d[0] + r[1] * d[1] + r[2] * d[2];
+    *rwy = r[3] * d[0] + r[4] * d[1] + r[5] * d[2];
+    *rwz = r[6] * d[0] + r[7] * d[1] + r[8] * d[2];
 }
 
 static void ob_lidar_scan(const float *input_obs, const float r[9], float py, ob_scan *s) {

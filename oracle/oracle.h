@@ -57,6 +57,9 @@ void orc_diagnostics_env(const float *obs, const uint8_t *cameras, uint32_t *dia
 void orc_onboard_env(const float *obs, const float *mission,
                      float *tactical24, float *prior15, float *diag4);
 
+/* Body-frame direction of onboard ray head*768 + el*128 + azi. */
+void orc_onboard_ray_dir(int ray, float *xyz);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,125 @@
+"""GPU parity of the onboard tactical (24) / prior (15) features, through the
+C-ABI entry tb_hip_onboard_tactical_prior_device, against the CPU oracle and
+the reference's own 40 goldens (tests/test_onboard_features.cu:55-85).
+
+Classes: the scan results (closest return, its ray, corridor minimum, cluster
+count) are bit-exact; tactical and prior values within 5e-5 absolute (the
+reference test's tolerance), prior values inside [-1, 1].
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.test_onboard_oracle import GOLDEN, reference_rows
+from turbinator_c_amd import synth
+
+pytestmark = pytest.mark.gpu
+TOL = 5e-5
+
+
+def note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def run_onboard(torch, hip, obs, mission, with_diag=True):
+    b = obs.shape[0]
+    d_obs = torch.from_numpy(np.ascontiguousarray(obs)).cuda()
+    d_mis = torch.from_numpy(np.ascontiguousarray(mission)).cuda()
+    tac = torch.full((b, 24), float("nan"), dtype=torch.float32, device="cuda")
+    pri = torch.full((b, 15), float("nan"), dtype=torch.float32, device="cuda")
+    diag = torch.full((b, 4), float("nan"), dtype=torch.float32, device="cuda") \
+        if with_diag else None
+    s = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    assert hip.onboard_tactical_prior_device(d_obs, d_mis, tac, pri, diag, b, s) == 1
+    assert hip.synchronize(s) == 1
+    return tac.cpu().numpy(), pri.cpu().numpy(), None if diag is None else diag.cpu().numpy()
+
+
+def in_window(obs):
+    """LiDAR scaled into the controller's 0.35..11.5 m window."""
+    o = obs.copy()
+    lid = o[:, 48:4144]
+    o[:, 48:4144] = np.where(lid > 0, lid / 30.0 + 0.3, lid)
+    return o
+
+
+def compare(got, want, label):
+    """NaN where (and only where) the oracle gives NaN: extreme finite inputs
+    such as 3e38 overflow inside the reference's cannon solution and its
+    clamp propagates NaN (onboard_features.cuh:7)."""
+    (gt, gp, gd), (wt, wp, wd) = got, want
+    for g, w, name in ((gt, wt, "tactical"), (gp, wp, "prior")):
+        assert np.array_equal(np.isnan(g), np.isnan(w)), f"{label}: {name} NaN pattern differs"
+        assert np.all(np.isfinite(g) | np.isnan(g)), f"{label}: {name} has an infinity"
+    gt, wt = np.nan_to_num(gt), np.nan_to_num(wt)
+    gp, wp = np.nan_to_num(gp), np.nan_to_num(wp)
+    assert np.all(np.abs(gp) <= 1.0), label
+    assert np.array_equal(gd.view(np.uint32), wd.view(np.uint32)), \
+        f"{label}: scan diagnostics differ at envs {np.argwhere((gd != wd).any(1))[:5].ravel()}"
+    dt = np.abs(gt - wt)
+    dp = np.abs(gp - wp)
+    bad_t = np.argwhere(dt > TOL)
+    bad_p = np.argwhere(dp > TOL)
+    assert not bad_t.size, f"{label}: tactical {bad_t[:3]} gpu {gt[tuple(bad_t[0])]} " \
+                           f"cpu {wt[tuple(bad_t[0])]}"
+    assert not bad_p.size, f"{label}: prior {bad_p[:3]} gpu {gp[tuple(bad_p[0])]} " \
+                           f"cpu {wp[tuple(bad_p[0])]}"
+    return {"tactical_max_abs": float(dt.max()), "prior_max_abs": float(dp.max()),
+            "prior_exact_frac": float((gp.view(np.uint32) == wp.view(np.uint32)).mean())}
+
+
+def test_reference_goldens_on_gpu(torch_cuda, hip):
+    note("onboard reference rows (40 goldens)")
+    obs, mission = reference_rows()
+    tac, pri, diag = run_onboard(torch_cuda, hip, obs, mission)
+    res = np.concatenate([tac, pri], axis=1)
+    for row, idx, want in GOLDEN:
+        got = res[row, idx]
+        assert np.isfinite(got) and abs(got - np.float32(want)) <= TOL, (row, idx, got, want)
+    assert np.all(np.abs(pri) <= 1.00001)
+    stats = compare((tac, pri, diag), oracle.onboard(obs, mission), "rows")
+    note(f"rows stats {stats}")
+
+
+@pytest.mark.parametrize("variant,batch", [(synth.ORDINARY, 4096), (synth.TIED_MINIMA, 1024),
+                                           (synth.CLAMP_LIMITS, 1024)])
+def test_random_batches(torch_cuda, hip, variant, batch):
+    note(f"onboard variant {variant}, {batch} envs")
+    b = synth.make_batch(batch, seed=300 + variant, variant=variant, threads=16)
+    obs = in_window(b.obs)
+    got = run_onboard(torch_cuda, hip, obs, b.mission)
+    stats = compare(got, oracle.onboard(obs, b.mission), f"variant{variant}")
+    note(f"variant {variant} stats {stats}")
+
+
+def test_special_values(torch_cuda, hip):
+    note("onboard non-finite inputs")
+    b = synth.make_batch(512, seed=17, variant=synth.SPECIAL)
+    obs = in_window(b.obs)
+    got = run_onboard(torch_cuda, hip, obs, b.mission)
+    compare(got, oracle.onboard(obs, b.mission), "special")
+
+
+def test_without_diag_and_sizes(torch_cuda, hip):
+    note("onboard without diag, ragged batch 1 and 1000")
+    for n in (1, 1000):
+        b = synth.make_batch(n, seed=n)
+        obs = in_window(b.obs)
+        tac, pri, _ = run_onboard(torch_cuda, hip, obs, b.mission, with_diag=False)
+        wt, wp, _ = oracle.onboard(obs, b.mission)
+        assert np.abs(tac - wt).max() <= TOL and np.abs(pri - wp).max() <= TOL
+
+
+def test_argument_validation(hip):
+    lib = hip.hip_lib()
+    import ctypes
+    d = ctypes.c_void_p(256)
+    assert lib.tb_hip_onboard_tactical_prior_device(None, d, d, d, None, 1, None) == 0
+    assert lib.tb_hip_onboard_tactical_prior_device(d, d, d, None, None, 1, None) == 0
+    assert lib.tb_hip_onboard_tactical_prior_device(d, d, d, d, None, 0, None) == 0

@@ -1,0 +1,143 @@
+"""Pins the onboard tactical/prior oracle (oracle/onboard_oracle.c).
+
+The reference holds four fixture rows (hover, slalom, BWB cruise, arena) and
+40 golden values at 5e-5, plus a [-1, 1] bound on all prior outputs
+(tests/test_onboard_features.cu:19-39,55-85).  The rows are rebuilt here from
+that description as data; the goldens are the reference's numbers.  Further
+checks are invariants of the controller that a plausible restatement mistake
+breaks (binary outputs, gated outputs, the LiDAR minimum as brute force).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from turbinator_c_amd import synth
+
+# (row, index into tactical[24] ++ prior[15], expected) from the reference test.
+GOLDEN = [
+    (0, 3, 0.0180000067), (0, 16, 0.148885041), (0, 19, 0.999999881),
+    (0, 20, 0.116912015), (0, 23, -0.707106769),
+    (0, 24, -0.287516475), (0, 26, 0.476842999), (0, 32, -0.382895738),
+    (0, 34, 0.382895738), (0, 38, -0.800000012),
+    (1, 12, 0.458358645), (1, 13, -0.313454777), (1, 15, 0.353995144),
+    (1, 20, 0.704012096), (1, 21, 0.718363643),
+    (1, 24, 0.476842999), (1, 25, -0.178828716), (1, 27, 0.0291560888),
+    (1, 32, 0.382895738), (1, 33, -0.107192054),
+    (2, 8, -0.209403276), (2, 10, 0.959999979), (2, 12, 0.319995612),
+    (2, 16, 0.977306247), (2, 19, -0.396981865),
+    (2, 24, -0.610540390), (2, 26, -0.610540390),
+    (2, 32, 0.541728497), (2, 33, 0.00769173447),
+    (3, 8, -0.0806194842), (3, 9, 0.416533887), (3, 10, 0.899999976),
+    (3, 12, -0.309927940), (3, 16, 0.988346934),
+    (3, 24, -0.100000024), (3, 26, -0.100000024),
+    (3, 32, -0.666666687), (3, 33, -0.345075011),
+    (3, 36, 1.0), (3, 37, 0.467838049),
+]
+
+
+def reference_rows():
+    """The four rows of tests/test_onboard_features.cu:19-39."""
+    obs = np.zeros((4, 4148), np.float32)
+    mission = np.zeros((4, 10), np.float32)
+    for r in range(4):
+        o = obs[r]
+        o[2] = 8.0; o[6] = 1.0; o[40] = 0.6; o[47] = 1.0
+        o[16:20] = 0.5
+        o[24:28] = 1.0
+    obs[0, 3] = 1.0
+    o, m = obs[1], mission[1]
+    o[0] = 5.0; o[1] = 0.4; o[3] = 2.0; o[4] = -0.2
+    o[48 + 2 * 128 + 3] = 5.0
+    o[48 + 2 * 128 + 4] = 5.1
+    m[4] = 1.0; m[7] = 0.3; m[8] = -0.2; m[9] = 0.1
+    o, m = obs[2], mission[2]
+    o[0] = 80.0; o[2] = 60.0; o[3] = 15.0; o[5] = -0.3
+    o[6] = 0.98; o[7] = 0.10; o[8] = 0.10; o[9] = 0.05
+    m[0] = 0.5; m[2] = 0.5; m[4] = 1.0
+    m[7] = 0.2; m[8] = 0.05; m[9] = 0.1
+    o, m = obs[3], mission[3]
+    o[0] = 200.0; o[2] = 40.0; o[3] = 20.0; o[4] = 1.0
+    o[6] = 0.9; o[7] = 0.1; o[8] = -0.2; o[9] = 0.3
+    m[4] = -0.5; m[5] = 0.8; m[6] = 1.0
+    m[7] = -0.3; m[8] = 0.1
+    return obs, mission
+
+
+def onboard(obs: np.ndarray, mission: np.ndarray):
+    lib = oracle.lib()
+    b = obs.shape[0]
+    tac = np.empty((b, 24), np.float32)
+    pri = np.empty((b, 15), np.float32)
+    diag = np.empty((b, 4), np.float32)
+    for e in range(b):
+        lib.orc_onboard_env(np.ascontiguousarray(obs[e]).ctypes.data,
+                            np.ascontiguousarray(mission[e]).ctypes.data,
+                            tac[e].ctypes.data, pri[e].ctypes.data, diag[e].ctypes.data)
+    return tac, pri, diag
+
+
+def test_reference_goldens():
+    obs, mission = reference_rows()
+    tac, pri, _ = onboard(obs, mission)
+    result = np.concatenate([tac, pri], axis=1)
+    for row, idx, want in GOLDEN:
+        got = result[row, idx]
+        assert np.isfinite(got) and abs(got - np.float32(want)) <= 5e-5, (row, idx, got, want)
+    assert np.all(np.isfinite(pri)) and np.all(np.abs(pri) <= 1.00001)
+
+
+def test_bounds_and_binary_outputs_on_random_inputs():
+    b = synth.make_batch(256, seed=21)
+    # Scale LiDAR into the controller's 0.35..11.5 m window so the scans act.
+    obs = b.obs.copy()
+    lid = obs[:, 48:4144]
+    obs[:, 48:4144] = np.where(lid > 0, lid / 30.0 + 0.3, lid)
+    tac, pri, diag = onboard(obs, b.mission)
+    assert np.all(np.isfinite(tac)) and np.all(np.isfinite(pri))
+    assert np.all(np.abs(pri) <= 1.0)
+    assert set(np.unique(tac[:, 11])) <= {0.0, 1.0}
+    assert set(np.unique(tac[:, 22])) <= {-1.0, 1.0}
+    assert set(np.unique(np.abs(pri[:, 14]))) <= {np.float32(0.8)}
+
+
+def test_lidar_minimum_is_first_in_scan_order():
+    """diag[0..1]: the closest in-window return over elevations 0..3 of both
+    heads, first in scan order on ties (brute force on the input)."""
+    b = synth.make_batch(64, seed=5, variant=synth.TIED_MINIMA)
+    obs = b.obs.copy()
+    lid = obs[:, 48:4144]
+    obs[:, 48:4144] = np.where(lid > 0, lid / 30.0, lid)
+    _, _, diag = onboard(obs, b.mission)
+    for e in range(64):
+        best, best_ray = 30.0, -1
+        for head in range(2):
+            for el in range(4):
+                for azi in range(128):
+                    r = obs[e, 48 + (head * 16 + el) * 128 + azi]
+                    if 0.35 < r < 11.5 and r < best:
+                        best, best_ray = r, head * 768 + el * 128 + azi
+        assert diag[e, 0] == np.float32(best) and int(diag[e, 1]) == best_ray
+
+
+def test_cannon_and_bwb_outputs_gated_by_mission():
+    obs, mission = reference_rows()
+    _, pri, _ = onboard(obs, mission)
+    # Rows 0 and 1 are neither arena nor BWB: cannon az/el are exactly 0.
+    assert np.all(pri[:2, 12:14] == 0.0)
+
+
+def test_device_ray_table_matches_oracle_rays():
+    """The table baked into the HIP library (generated with the host libm at
+    build time) holds exactly the oracle's per-ray directions."""
+    import re
+    inc = oracle.HERE.parent / "_build" / "onboard_rays.inc"
+    if not inc.exists():
+        pytest.skip("library not built here (_build/onboard_rays.inc missing)")
+    vals = [float.fromhex(v) for v in re.findall(r"(-?0x[0-9a-fp.+-]+)", inc.read_text())]
+    table = np.array(vals, np.float32).reshape(1536, 3)
+    want = oracle.onboard_ray_table()
+    assert np.array_equal(table.view(np.uint32), want.view(np.uint32))

@@ -37,7 +37,7 @@ HIP_FLAGS = [
 C_FLAGS = ["-O2", "-std=c11", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
            f"-I{ROCM / 'include'}", f"-I{INCLUDE}"]
 
-HIP_SOURCES = ["features.hip"]
+HIP_SOURCES = ["features.hip", "onboard.hip"]
 HOST_C_SOURCES = ["feature_batch.c"]
 
 LIB_HIP = PKG / "libturbinator_hip.so"
@@ -61,12 +61,26 @@ def hipcc() -> str:
     return exe
 
 
+def generate_ray_table() -> Path:
+    """onboard_rays.inc: ray directions evaluated with the host libm (no
+    optimisation, so no compile-time folding replaces the libm calls)."""
+    BUILD.mkdir(exist_ok=True)
+    exe = BUILD / "gen_ray_table"
+    _run(["gcc", "-O0", "-std=c11", "-fno-builtin", "-ffp-contract=off", "-o", str(exe),
+          str(CSRC / "gen_ray_table.c"), "-lm"])
+    inc = BUILD / "onboard_rays.inc"
+    text = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+    inc.write_text(text)
+    return inc
+
+
 def build_hip_library() -> Path:
     BUILD.mkdir(exist_ok=True)
+    generate_ray_table()
     objs = []
     for src in HIP_SOURCES:
         obj = BUILD / (Path(src).stem + ".hip.o")
-        _run([hipcc(), *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)])
+        _run([hipcc(), *HIP_FLAGS, f"-I{BUILD}", "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(obj)
     for src in HOST_C_SOURCES:
         obj = BUILD / (Path(src).stem + ".c.o")

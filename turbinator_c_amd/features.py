@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .native import CAMERA_BYTES, FEATURE_DIM, MISSION_DIM, OBS_DIM, hip_lib
+from .native import CAMERA_BYTES, FEATURE_DIM, MISSION_DIM, OBS_DIM, hip_lib  # noqa: F401
 
 
 def _dev(x) -> int | None:
@@ -50,6 +50,14 @@ def lidar_transform_device(ranges, out, count: int, stream=None) -> int:
     """tb_hip_lidar_transform_device (hip_features.h)."""
     return hip_lib().tb_hip_lidar_transform_device(_dev(ranges), _dev(out), count,
                                                    _stream(stream))
+
+
+def onboard_tactical_prior_device(obs, mission, tactical, prior, diag, batch_size: int,
+                                  stream=None) -> int:
+    """tb_hip_onboard_tactical_prior_device (hip_features.h)."""
+    return hip_lib().tb_hip_onboard_tactical_prior_device(
+        _dev(obs), _dev(mission), _dev(tactical), _dev(prior), _dev(diag), batch_size,
+        _stream(stream))
 
 
 def synchronize(stream=None) -> int:
@@ -104,4 +112,4 @@ def feature_batch_error(handle) -> str:
 
 
 __all__ = ["extract_features_device", "extract_features_strided_device",
-           "lidar_transform_device", "synchronize", "FeatureBatch", "feature_batch_error"]
+           "lidar_transform_device", "onboard_tactical_prior_device", "synchronize", "FeatureBatch", "feature_batch_error"]

@@ -38,6 +38,8 @@ HIP_SIGNATURES = {
         (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p,
                  c_size_t, c_void_p]),
     "tb_hip_lidar_transform_device": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "tb_hip_onboard_tactical_prior_device":
+        (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
 }
 
 SYNTH_SIGNATURES = {
