@@ -142,6 +142,107 @@ def verify_sample(torch, sets, host0) -> dict:
     return assert_feature_parity(got, want, "bench-sample")
 
 
+def _events_time(torch, launch, steps: int, warmup: int) -> float:
+    """Seconds per call of `launch(i)` on the current stream (HIP events)."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        launch(i, stream)
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(steps):
+        launch(i, stream)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / 1e3 / steps
+
+
+def _report(name: str, per_call: float, envs: int, bytes_per_env: int | None, **extra) -> dict:
+    r = {"workload": name, "us_per_call": round(per_call * 1e6, 2),
+         "envs_per_s": round(envs / per_call, 1)}
+    if bytes_per_env:
+        gbs = bytes_per_env * envs / per_call / 1e9
+        r.update(bytes_per_env=bytes_per_env, achieved_GBs=round(gbs, 1),
+                 frac_of_peak=round(gbs / HBM_PEAK_GBS, 4))
+    r.update(extra)
+    log("[suite] " + json.dumps(r))
+    return r
+
+
+def suite(torch, sets, threads: int, steps: int) -> list:
+    """Secondary workloads, printed to stderr (the stdout line is the headline)."""
+    from turbinator_c_amd import features, synth
+    out = []
+    # fp32 depth cameras: the configurations' literal 4x64x64 fp32 cameras.
+    dsets = []
+    for k in range(3):
+        b = synth.make_batch(BATCH, seed=142 + k, with_depth=True, threads=threads)
+        dsets.append((torch.from_numpy(b.obs).cuda(), torch.from_numpy(b.mission).cuda(),
+                      torch.from_numpy(b.depth).cuda(),
+                      torch.empty((BATCH, 142), dtype=torch.float32, device="cuda")))
+        del b
+
+    def depth_call(i, s):
+        o, m, d, f = dsets[i % 3]
+        assert features.extract_features_depth_device(o, m, d, f, BATCH, s) == 1
+    out.append(_report("config 3 with fp32 depth cameras (16,384 envs, 3 rotating sets)",
+                       _events_time(torch, depth_call, steps, 5), BATCH,
+                       OBS_B + MISSION_B + 4 * CAMERA_B + OUT_B))
+    del dsets
+
+    diag = torch.empty((BATCH, 224), dtype=torch.int32, device="cuda")
+
+    def diag_call(i, s):
+        o, m, c, f = sets[i % len(sets)]
+        assert features.extract_features_diagnostics_device(o, m, c, f, diag, BATCH, s) == 1
+    out.append(_report("config 3 + diagnostics (224 words/env)",
+                       _events_time(torch, diag_call, steps, 5), BATCH, BYTES_PER_ENV + 896))
+
+    tac = torch.empty((BATCH, 24), dtype=torch.float32, device="cuda")
+    pri = torch.empty((BATCH, 15), dtype=torch.float32, device="cuda")
+
+    def onboard_call(i, s):
+        o, m, _, _ = sets[i % len(sets)]
+        assert features.onboard_tactical_prior_device(o, m, tac, pri, None, BATCH, s) == 1
+    out.append(_report("onboard tactical+prior (16,384 envs)",
+                       _events_time(torch, onboard_call, steps, 5), BATCH, None))
+
+    # Configuration 5: 65,536 replay records of 66,672 B, features in place.
+    n5, rec = 65536, 66672
+    buf = np.zeros(n5 * rec, np.uint8)
+    synth.fill_records(buf, n5, rec, 0, 16592, 16632, seed=77, threads=threads)
+    dbuf = torch.from_numpy(buf).cuda()
+    del buf
+    f5 = torch.empty((n5, 142), dtype=torch.float32, device="cuda")
+    base = dbuf.data_ptr()
+
+    def c5_call(i, s):
+        assert features.extract_features_strided_device(base, rec, base + 16592, rec,
+                                                        base + 16632, rec, f5, n5, s) == 1
+    out.append(_report("config 5: 65,536 replay records x 66,672 B, in place",
+                       _events_time(torch, c5_call, max(steps // 4, 10), 3), n5, BYTES_PER_ENV))
+    del dbuf, f5
+
+    # Host API, PCIe included (pageable copies, as the reference): batch 1024.
+    hb = synth.make_batch(1024, seed=9, threads=threads)
+    outh = np.empty((1024, 142), np.float32)
+    fb = features.FeatureBatch.create(0, 1024)
+    try:
+        for _ in range(3):
+            assert fb.extract_host(hb.obs, hb.mission, hb.cameras, 1024, outh) == 1
+        t0 = time.perf_counter()
+        reps = 20
+        for _ in range(reps):
+            assert fb.extract_host(hb.obs, hb.mission, hb.cameras, 1024, outh) == 1
+        per = (time.perf_counter() - t0) / reps
+    finally:
+        fb.destroy()
+    out.append(_report("host API tb_cuda_extract_features_host, 1,024 envs (PCIe-inclusive)",
+                       per, 1024, None, note="pageable host memory, synchronous"))
+    return out
+
+
 def cpu_baseline(host0, threads: int, budget_s: float) -> dict:
     """The CPU oracle (restatement of src/training/training.c:102-142,
     -O3 -std=c11) over the first environments of the same batch, on
@@ -183,6 +284,8 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=3, help="rotating input buffer sets")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--suite", action="store_true",
+                    help="also time the secondary workloads (stderr JSON lines)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after timing, run 1 GiB device copies (PMC calibration)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -214,6 +317,8 @@ def main() -> int:
     log(f"[bench] parity sample ok: {stats}")
     if args.copy_calibration:
         copy_calibration(torch)
+    if args.suite:
+        suite(torch, sets, threads, args.steps)
     bytes_per_call = BYTES_PER_ENV * BATCH
     achieved = bytes_per_call / per_call / 1e9
     traffic = None

@@ -41,6 +41,37 @@ int tb_hip_extract_features_strided_device(const void *obs, size_t obs_stride,
                                            float *features,
                                            size_t batch_size, void *stream);
 
+/* The 142 features of tb_cuda_extract_features_device plus, from the same
+ * single pass, per-environment diagnostics that have no counterpart in the
+ * reference feature vector (training.c:107-141).  `diagnostics` receives
+ * [batch, 224] 32-bit words:
+ *   0..63    LiDAR sector minimum range over valid bins (float bits; -1.0 if
+ *            the sector has none); valid = finite and >= 0
+ *   64..127  LiDAR argmin: bin index 0..4095 of the first minimum in the
+ *            reference scan order (row outer, bin inner); 0xffffffff if none
+ *   128..191 LiDAR valid-bin count per sector
+ *   192..207 camera quadrant minimum byte (0 when cameras is NULL)
+ *   208..223 camera quadrant occupancy: bytes != 0 (0 when cameras is NULL)
+ * Sector s = head*32 + el_sector*8 + az_sector and quadrant
+ * q = cam*4 + qy*2 + qx, the feature vector's orders.  Same argument rules as
+ * tb_cuda_extract_features_device; diagnostics must be 4-byte aligned. */
+int tb_hip_extract_features_diagnostics_device(const float *obs, const float *mission,
+                                               const unsigned char *cameras,
+                                               float *features, void *diagnostics,
+                                               size_t batch_size, void *stream);
+
+/* The 142 features with the cameras given as fp32 depth in metres
+ * ([batch, 16384] floats, 16-byte aligned), the 4x64x64 fp32 cameras of the
+ * benchmark configurations.  Each pixel is quantised to the luma byte the
+ * reference ABI carries, 255 * (1 - clamp(d, 0, 200) / 200) rounded half to
+ * even (far plane 200 m -> 0; non-finite -> 0 m), then features 126..141
+ * are the reference quadrant means of those bytes (training.c:128-141).
+ * Returns 0 for NULL pointers, a misaligned depth array, batch 0 or above
+ * 0x7fffffff. */
+int tb_hip_extract_features_depth_device(const float *obs, const float *mission,
+                                         const float *depth, float *features,
+                                         size_t batch_size, void *stream);
+
 /* Per-bin LiDAR transform of the feature kernel, elementwise over `count`
  * floats: -1 for non-finite or negative ranges, otherwise
  * log1p(min(r,120)) / log1pf(120) (reference training.c:65-68).  Exposed so

@@ -40,6 +40,8 @@ def lib() -> ctypes.CDLL:
         l.orc_lidar_feature_array.restype = None
         l.orc_depth_to_luma.argtypes = [c_float]
         l.orc_depth_to_luma.restype = ctypes.c_uint8
+        l.orc_depth_to_luma_array.argtypes = [c_void_p, c_void_p, c_size_t]
+        l.orc_depth_to_luma_array.restype = None
         l.orc_diagnostics_env.argtypes = [c_void_p, c_void_p, c_void_p]
         l.orc_diagnostics_env.restype = None
         l.orc_onboard_env.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
@@ -129,6 +131,13 @@ def onboard_ray_table() -> np.ndarray:
     out = np.empty((1536, 3), np.float32)
     for ray in range(1536):
         lib().orc_onboard_ray_dir(ray, out[ray].ctypes.data)
+    return out
+
+
+def depth_to_luma(depth: np.ndarray) -> np.ndarray:
+    d = np.ascontiguousarray(depth, np.float32)
+    out = np.empty(d.shape, np.uint8)
+    lib().orc_depth_to_luma_array(_p(d), _p(out), d.size)
     return out
 
 

@@ -132,6 +132,10 @@ uint8_t orc_depth_to_luma(float depth_m) {
     return (uint8_t)lrintf(v);
 }
 
+void orc_depth_to_luma_array(const float *depth, uint8_t *luma, size_t n) {
+    for (size_t i = 0; i < n; ++i) luma[i] = orc_depth_to_luma(depth[i]);
+}
+
 void orc_diagnostics_env(const float *obs, const uint8_t *cameras, uint32_t *diag) {
     float *fmin = (float *)(void *)diag;
     int32_t *arg = (int32_t *)(void *)(diag + 64);

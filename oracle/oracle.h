@@ -42,6 +42,7 @@ void orc_lidar_feature_array(const float *in, float *out, size_t n, int threads)
 
 /* Depth (metres) -> luma byte map used for fp32-depth camera inputs. */
 uint8_t orc_depth_to_luma(float depth_m);
+void orc_depth_to_luma_array(const float *depth, uint8_t *luma, size_t n);
 
 /* Per-environment diagnostics with no counterpart in the 142-vector:
  * words 0..63    LiDAR sector minimum over valid bins (float, -1 if none)

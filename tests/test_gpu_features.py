@@ -231,3 +231,76 @@ def test_reference_test_binary_drop_in():
     note(f"drop-in: rc={proc.returncode} out={proc.stdout.strip()} err={proc.stderr.strip()}")
     assert proc.returncode == 0
     assert "matches C11 extraction" in proc.stdout
+
+
+def run_diag(torch, hip, obs, mission, cameras):
+    b = obs.shape[0]
+    d_obs = torch.from_numpy(np.ascontiguousarray(obs)).cuda()
+    d_mis = torch.from_numpy(np.ascontiguousarray(mission)).cuda()
+    d_cam = None if cameras is None else torch.from_numpy(np.ascontiguousarray(cameras)).cuda()
+    out = torch.full((b, 142), float("nan"), dtype=torch.float32, device="cuda")
+    diag = torch.full((b, 224), -7, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    assert hip.extract_features_diagnostics_device(d_obs, d_mis, d_cam, out, diag, b, s) == 1
+    assert hip.synchronize(s) == 1
+    return out.cpu().numpy(), diag.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("variant,batch", [(synth.EDGE_QUARTERS, 4096), (synth.SPECIAL, 512),
+                                           (synth.ORDINARY, 1024)])
+def test_diagnostics_bit_exact(torch_cuda, hip, variant, batch):
+    note(f"diagnostics variant {variant}, {batch} envs")
+    b = synth.make_batch(batch, seed=4242, variant=variant, threads=16)
+    feats, diag = run_diag(torch_cuda, hip, b.obs, b.mission, b.cameras)
+    assert_feature_parity(feats, oracle.features(b.obs, b.mission, b.cameras), "diag-features")
+    want = oracle.diagnostics(b.obs, b.cameras)
+    bad = np.argwhere(diag != want)
+    assert not bad.size, f"diag word {bad[0]}: gpu {diag[tuple(bad[0])]:#x} " \
+                         f"cpu {want[tuple(bad[0])]:#x} ({len(bad)} words differ)"
+    if variant == synth.EDGE_QUARTERS:
+        assert np.all(diag[:1024, 64:128] == 0xffffffff)          # Q1: no valid bin
+        assert np.all(diag[1024:2048, 192:208] == 207)            # Q2: constant camera
+
+
+def test_diagnostics_null_cameras(torch_cuda, hip):
+    note("diagnostics, NULL cameras")
+    b = synth.make_batch(128, seed=5)
+    feats, diag = run_diag(torch_cuda, hip, b.obs, b.mission, None)
+    assert np.array_equal(diag, oracle.diagnostics(b.obs, None))
+    assert np.all(diag[:, 192:] == 0)
+
+
+def run_depth(torch, hip, obs, mission, depth):
+    b = obs.shape[0]
+    d_obs = torch.from_numpy(np.ascontiguousarray(obs)).cuda()
+    d_mis = torch.from_numpy(np.ascontiguousarray(mission)).cuda()
+    d_dep = torch.from_numpy(np.ascontiguousarray(depth)).cuda()
+    out = torch.full((b, 142), float("nan"), dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    assert hip.extract_features_depth_device(d_obs, d_mis, d_dep, out, b, s) == 1
+    assert hip.synchronize(s) == 1
+    return out.cpu().numpy()
+
+
+def test_depth_cameras_config2(torch_cuda, hip):
+    note("fp32 depth cameras, 1024 envs")
+    b = synth.make_batch(1024, seed=42, with_depth=True, threads=16)
+    got = run_depth(torch_cuda, hip, b.obs, b.mission, b.depth)
+    want = oracle.features(b.obs, b.mission, oracle.depth_to_luma(b.depth))
+    assert_feature_parity(got, want, "depth")
+
+
+def test_depth_cameras_special_values(torch_cuda, hip):
+    note("fp32 depth cameras, special depth values")
+    b = synth.make_batch(64, seed=8, with_depth=True)
+    depth = b.depth.copy()
+    rng = np.random.default_rng(1)
+    specials = np.array([np.nan, np.inf, -np.inf, -0.0, 0.0, -3.0, 200.0, 250.0, 1e-40, 3e38,
+                         37.5, 100.0], np.float32)
+    mask = rng.random(depth.shape) < 0.2
+    depth[mask] = rng.choice(specials, mask.sum())
+    got = run_depth(torch_cuda, hip, b.obs, b.mission, depth)
+    want = oracle.features(b.obs, b.mission, oracle.depth_to_luma(depth))
+    assert_feature_parity(got, want, "depth-special")

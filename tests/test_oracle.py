@@ -177,3 +177,36 @@ def test_golden_c4_covers_every_quarter():
     assert sorted({1 + e * 4 // C4_BATCH for e in C4_ENVS}) == [1, 2, 3, 4]
     obs, mission, cams = envs_inputs(42, C4_ENVS[:4], [1] * 4)
     assert np.all(obs[:, 48:4144] == -1.0)
+
+
+def numpy_diagnostics(obs: np.ndarray, cameras: np.ndarray | None) -> np.ndarray:
+    """Independent formulation of orc_diagnostics_env with numpy reshapes:
+    np.argmin returns the first occurrence, in scan order (row, bin)."""
+    b = obs.shape[0]
+    out = np.zeros((b, 224), np.uint32)
+    lid = obs[:, 48:4144].reshape(b, 2, 4, 4, 8, 16)          # env,head,es,el,as,az
+    sec = lid.transpose(0, 1, 2, 4, 3, 5).reshape(b, 64, 64)  # env,sector,(el,az)
+    binidx = np.arange(4096).reshape(2, 4, 4, 8, 16).transpose(0, 1, 3, 2, 4).reshape(64, 64)
+    valid = np.isfinite(sec) & (sec >= 0)
+    masked = np.where(valid, sec, np.inf)
+    arg = np.argmin(masked, axis=2)
+    anyv = valid.any(axis=2)
+    mins = np.take_along_axis(sec, arg[..., None], axis=2)[..., 0]
+    out[:, 0:64] = np.where(anyv, mins, np.float32(-1.0)).astype(np.float32).view(np.uint32)
+    out[:, 64:128] = np.where(anyv, binidx[np.arange(64)[None, :], arg], -1).astype(
+        np.int32).view(np.uint32)
+    out[:, 128:192] = valid.sum(axis=2)
+    if cameras is not None:
+        q = cameras.reshape(b, 4, 2, 32, 2, 32).transpose(0, 1, 2, 4, 3, 5).reshape(b, 16, 1024)
+        out[:, 192:208] = q.min(axis=2)
+        out[:, 208:224] = (q != 0).sum(axis=2)
+    return out
+
+
+@pytest.mark.parametrize("variant", [0, 3, 4, 5])
+def test_oracle_diagnostics_match_numpy(variant):
+    b = synth.make_batch(16, seed=70 + variant, variant=variant)
+    for cams in (b.cameras, None):
+        got = oracle.diagnostics(b.obs, cams)
+        want = numpy_diagnostics(b.obs, cams)
+        assert np.array_equal(got, want)

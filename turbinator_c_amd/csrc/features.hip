@@ -59,7 +59,10 @@ struct Rows {
     size_t mission_stride;
     const unsigned char *cameras;
     size_t camera_stride;
+    const float *depth;  // fp32 depth cameras [batch, 16384] metres (DEPTH kernels)
+    size_t depth_stride;
     float *out;
+    uint32_t *diag;  // optional [batch, 224] diagnostics words (DIAG kernels)
     size_t batch;
 };
 
@@ -157,14 +160,71 @@ __device__ __forceinline__ unsigned sum_same_qx(unsigned v) {
     return v;
 }
 
+// Depth (metres) -> luma byte: 255 * (1 - clamp(d, 0, 200) / 200), rounded
+// half to even; non-finite depth counts as 0 m.  The quotient is formed as
+// (float)((double)x * RN(1/200)), which equals the IEEE quotient x / 200.0f
+// for every float x in [0, 200] (checked exhaustively by
+// tests/csrc/check_div_by_constant.c), so the bytes are bit-exact.
+__device__ __forceinline__ unsigned depth_luma(float depth_m) {
+    const float d = clamp_ref(finite_or_zero(depth_m), 0.0f, 200.0f);
+    const float q = (float)((double)d * (1.0 / 200.0));
+    return (unsigned)__builtin_rintf(255.0f * (1.0f - q));
+}
+
+// Sum over the 32 lanes that share lane bit 3 (column half of a 64-float
+// depth row read as 16 lanes x float4).
+__device__ __forceinline__ unsigned sum_same_bit3(unsigned v) {
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ __forceinline__ unsigned bytes_min(u32x4 w, unsigned m) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) m = min(m, (w[d] >> (8 * b)) & 0xffu);
+    return m;
+}
+
+// Bytes != 0: the high bit of each byte of ((x & 0x7f..) + 0x7f..) | x is set
+// exactly when that byte is nonzero (no carry crosses a byte).
+__device__ __forceinline__ unsigned bytes_nonzero(u32x4 w, unsigned n) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+        n += __builtin_popcount((((w[d] & 0x7f7f7f7fu) + 0x7f7f7f7fu) | w[d]) & 0x80808080u);
+    return n;
+}
+
+__device__ __forceinline__ unsigned min_same_qx(unsigned v) {
+    v = min(v, __shfl_xor(v, 1));
+    v = min(v, __shfl_xor(v, 4));
+    v = min(v, __shfl_xor(v, 8));
+    v = min(v, __shfl_xor(v, 16));
+    v = min(v, __shfl_xor(v, 32));
+    return v;
+}
+
 // LV: floats per LiDAR load (4, 2 or 1 from the row alignment).
 // CV: bytes per camera load (16, 8, 4 or 1 from the row alignment).
-template <int LV, int CV>
+// DIAG: also write the per-environment diagnostics (no reference
+// counterpart): LiDAR sector minimum / first argmin / valid count and camera
+// quadrant minimum byte / nonzero count, from the same loads.
+// DEPTH: cameras arrive as fp32 depth and are quantised to luma bytes in
+// registers (the configurations' 4x64x64 fp32 cameras).
+template <int LV, int CV, bool DIAG, bool DEPTH = false>
 __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
     __shared__ f32x4 stage[16 * kStagePitch];
+    // DIAG partials per (chunk, sector): minimum valid range and
+    // (first argmin bin + 1) | (valid count << 16).
+    __shared__ float dmin[DIAG ? 16 * kStagePitch : 1];
+    __shared__ unsigned dinfo[DIAG ? 16 * kStagePitch : 1];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const bool has_cameras = rows.cameras != nullptr;
+    const bool has_cameras = DEPTH || rows.cameras != nullptr;
 
     // Stage position of this lane's float4 for each of the wave's 4 loads:
     // LiDAR float4 index i*64 + lane (i = 4w + k) is row (i%8)*2 + lane/32
@@ -188,7 +248,7 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
         u32x4 px[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) v[k] = load_lidar4<LV>(lidar + (4 * w + k) * 256 + 4 * lane);
-        if (has_cameras) {
+        if (!DEPTH && has_cameras) {
             // Camera w, rows 16k + lane/4, bytes 16*(lane%4)..+15.
             const unsigned char *cam = rows.cameras + env * rows.camera_stride + w * 4096;
 #pragma unroll
@@ -204,10 +264,53 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
             f.w = lidar_bin_feature(v[k].w);
             stage[unit[k]] = f;
         }
+        if constexpr (DIAG) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int i = 4 * w + k;
+                const int bin0 = (i >> 3) * 2048 + (((i & 7) << 1) + (lane >> 5)) * 128 +
+                                 ((lane & 31) >> 2) * 16 + 4 * (lane & 3);
+                float best = 0.0f;
+                unsigned first = 0u, count = 0u;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float r = v[k][e];
+                    if ((r >= 0.0f) && (r < __builtin_huge_valf())) {
+                        ++count;
+                        if (first == 0u || r < best) { best = r; first = bin0 + e + 1; }
+                    }
+                }
+                dmin[unit[k]] = best;
+                dinfo[unit[k]] = first | (count << 16);
+            }
+        }
 
         // Quadrant (cam w, qy, qx = lane bit 1): loads k = 0,1 cover rows
         // 0..31 (qy 0), k = 2,3 rows 32..63 (qy 1).  training.c:128-141.
-        if (has_cameras) {
+        if constexpr (DEPTH) {
+            // Camera w as 4096 floats: load k covers rows 4k + lane/16,
+            // columns 4*(lane%16)..+3, so qy = k/8 and qx = lane bit 3.
+            const float *cam = reinterpret_cast<const float *>(
+                reinterpret_cast<const unsigned char *>(rows.depth) + env * rows.depth_stride) +
+                w * 4096;
+            unsigned top = 0u, bottom = 0u;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const f32x4 d = __builtin_nontemporal_load(
+                    reinterpret_cast<const f32x4 *>(cam + k * 256 + 4 * lane));
+                const unsigned s4 =
+                    depth_luma(d.x) + depth_luma(d.y) + depth_luma(d.z) + depth_luma(d.w);
+                if (k < 8) top += s4;
+                else bottom += s4;
+            }
+            top = sum_same_bit3(top);
+            bottom = sum_same_bit3(bottom);
+            if (lane == 0 || lane == 8) {
+                const int qx = lane >> 3;
+                out[126 + w * 4 + qx] = (float)top / (1024.0f * 255.0f);
+                out[126 + w * 4 + 2 + qx] = (float)bottom / (1024.0f * 255.0f);
+            }
+        } else if (has_cameras) {
             const unsigned top = sum_same_qx(byte_sum(px[1], byte_sum(px[0], 0u)));
             const unsigned bottom = sum_same_qx(byte_sum(px[3], byte_sum(px[2], 0u)));
             if (lane == 0 || lane == 2) {
@@ -217,6 +320,25 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
             }
         } else if (lane < 4) {
             out[126 + w * 4 + lane] = 0.0f;
+        }
+        if constexpr (DIAG) {
+            uint32_t *diag = rows.diag + env * 224;
+            if (has_cameras) {
+                const unsigned top_min = min_same_qx(bytes_min(px[1], bytes_min(px[0], 255u)));
+                const unsigned bot_min = min_same_qx(bytes_min(px[3], bytes_min(px[2], 255u)));
+                const unsigned top_occ = sum_same_qx(bytes_nonzero(px[1], bytes_nonzero(px[0], 0u)));
+                const unsigned bot_occ = sum_same_qx(bytes_nonzero(px[3], bytes_nonzero(px[2], 0u)));
+                if (lane == 0 || lane == 2) {
+                    const int q = w * 4 + (lane >> 1);
+                    diag[192 + q] = top_min;
+                    diag[192 + q + 2] = bot_min;
+                    diag[208 + q] = top_occ;
+                    diag[208 + q + 2] = bot_occ;
+                }
+            } else if (lane < 4) {
+                diag[192 + w * 4 + lane] = 0u;
+                diag[208 + w * 4 + lane] = 0u;
+            }
         }
 
         __syncthreads();
@@ -232,6 +354,26 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
                 sum += f.w;
             }
             out[62 + lane] = sum / 64.0f;
+            if constexpr (DIAG) {
+                // Chunks in increasing c are in scan order (row outer, bin
+                // inner), so a strict < keeps the first minimum.
+                float best = 0.0f;
+                unsigned first = 0u, count = 0u;
+#pragma unroll
+                for (int c = 0; c < 16; ++c) {
+                    const unsigned info = dinfo[c * kStagePitch + lane];
+                    const float m = dmin[c * kStagePitch + lane];
+                    count += info >> 16;
+                    if ((info & 0xffffu) != 0u && (first == 0u || m < best)) {
+                        best = m;
+                        first = info & 0xffffu;
+                    }
+                }
+                uint32_t *diag = rows.diag + env * 224;
+                diag[lane] = first == 0u ? __float_as_uint(-1.0f) : __float_as_uint(best);
+                diag[64 + lane] = first == 0u ? 0xffffffffu : first - 1u;
+                diag[128 + lane] = count;
+            }
         } else if (w == 1 && lane < 62) {
             // training.c:107-112.
             float scalar;
@@ -267,14 +409,26 @@ int vector_bytes(const void *base, size_t stride, int widest) {
     return 1;
 }
 
-template <int LV>
+template <int LV, bool DIAG>
 void launch_lv(const Rows &rows, int cv, unsigned blocks, hipStream_t stream) {
     switch (cv) {
-    case 16: features_kernel<LV, 16><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
-    case 8: features_kernel<LV, 8><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
-    case 4: features_kernel<LV, 4><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
-    default: features_kernel<LV, 1><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
+    case 16: features_kernel<LV, 16, DIAG><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
+    case 8: features_kernel<LV, 8, DIAG><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
+    case 4: features_kernel<LV, 4, DIAG><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
+    default: features_kernel<LV, 1, DIAG><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
     }
+}
+
+template <bool DIAG>
+void launch_diag(const Rows &rows, int lv, int cv, unsigned blocks, hipStream_t stream) {
+    if (lv == 4) launch_lv<4, DIAG>(rows, cv, blocks, stream);
+    else if (lv == 2) launch_lv<2, DIAG>(rows, cv, blocks, stream);
+    else launch_lv<1, DIAG>(rows, cv, blocks, stream);
+}
+
+template <int LV>
+void launch_depth(const Rows &rows, unsigned blocks, hipStream_t stream) {
+    features_kernel<LV, 16, false, true><<<blocks, kBlockThreads, 0, stream>>>(rows);
 }
 
 int launch_features(const Rows &rows, hipStream_t stream) {
@@ -287,9 +441,12 @@ int launch_features(const Rows &rows, hipStream_t stream) {
     // unrelated earlier runtime call (e.g. selecting a missing device) is
     // not a launch failure.
     (void)hipGetLastError();
-    if (lv == 4) launch_lv<4>(rows, cv, blocks, stream);
-    else if (lv == 2) launch_lv<2>(rows, cv, blocks, stream);
-    else launch_lv<1>(rows, cv, blocks, stream);
+    if (rows.depth) {
+        if (lv == 4) launch_depth<4>(rows, blocks, stream);
+        else if (lv == 2) launch_depth<2>(rows, blocks, stream);
+        else launch_depth<1>(rows, blocks, stream);
+    } else if (rows.diag) launch_diag<true>(rows, lv, cv, blocks, stream);
+    else launch_diag<false>(rows, lv, cv, blocks, stream);
     return hipGetLastError() == hipSuccess;
 }
 
@@ -310,7 +467,32 @@ extern "C" int tb_cuda_extract_features_device(const float *device_obs,
     rows.mission_stride = 10 * sizeof(float);
     rows.cameras = device_cameras;
     rows.camera_stride = 16384;
+    rows.depth = nullptr;
+    rows.depth_stride = 0;
     rows.out = device_features;
+    rows.diag = nullptr;
+    rows.batch = batch_size;
+    return launch_features(rows, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int tb_hip_extract_features_diagnostics_device(const float *obs, const float *mission,
+                                                          const unsigned char *cameras,
+                                                          float *features, void *diagnostics,
+                                                          size_t batch_size, void *stream) {
+    if (!obs || !mission || !features || !diagnostics || batch_size == 0 ||
+        batch_size > kMaxBatch || (reinterpret_cast<uintptr_t>(diagnostics) & 3u) != 0)
+        return 0;
+    Rows rows;
+    rows.obs = reinterpret_cast<const unsigned char *>(obs);
+    rows.obs_stride = kObsDim * sizeof(float);
+    rows.mission = reinterpret_cast<const unsigned char *>(mission);
+    rows.mission_stride = 10 * sizeof(float);
+    rows.cameras = cameras;
+    rows.camera_stride = 16384;
+    rows.depth = nullptr;
+    rows.depth_stride = 0;
+    rows.out = features;
+    rows.diag = static_cast<uint32_t *>(diagnostics);
     rows.batch = batch_size;
     return launch_features(rows, reinterpret_cast<hipStream_t>(stream));
 }
@@ -333,7 +515,31 @@ extern "C" int tb_hip_extract_features_strided_device(const void *obs, size_t ob
     rows.mission_stride = mission_stride;
     rows.cameras = static_cast<const unsigned char *>(cameras);
     rows.camera_stride = camera_stride;
+    rows.depth = nullptr;
+    rows.depth_stride = 0;
     rows.out = features;
+    rows.diag = nullptr;
+    rows.batch = batch_size;
+    return launch_features(rows, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int tb_hip_extract_features_depth_device(const float *obs, const float *mission,
+                                                    const float *depth, float *features,
+                                                    size_t batch_size, void *stream) {
+    if (!obs || !mission || !depth || !features || batch_size == 0 || batch_size > kMaxBatch ||
+        (reinterpret_cast<uintptr_t>(depth) & 15u) != 0)
+        return 0;
+    Rows rows;
+    rows.obs = reinterpret_cast<const unsigned char *>(obs);
+    rows.obs_stride = kObsDim * sizeof(float);
+    rows.mission = reinterpret_cast<const unsigned char *>(mission);
+    rows.mission_stride = 10 * sizeof(float);
+    rows.cameras = nullptr;
+    rows.camera_stride = 0;
+    rows.depth = depth;
+    rows.depth_stride = 16384 * sizeof(float);
+    rows.out = features;
+    rows.diag = nullptr;
     rows.batch = batch_size;
     return launch_features(rows, reinterpret_cast<hipStream_t>(stream));
 }

@@ -46,6 +46,21 @@ def extract_features_strided_device(obs, obs_stride: int, mission, mission_strid
         _dev(features), batch_size, _stream(stream))
 
 
+def extract_features_diagnostics_device(obs, mission, cameras, features, diagnostics,
+                                        batch_size: int, stream=None) -> int:
+    """tb_hip_extract_features_diagnostics_device (hip_features.h)."""
+    return hip_lib().tb_hip_extract_features_diagnostics_device(
+        _dev(obs), _dev(mission), _dev(cameras), _dev(features), _dev(diagnostics), batch_size,
+        _stream(stream))
+
+
+def extract_features_depth_device(obs, mission, depth, features, batch_size: int,
+                                  stream=None) -> int:
+    """tb_hip_extract_features_depth_device (hip_features.h)."""
+    return hip_lib().tb_hip_extract_features_depth_device(
+        _dev(obs), _dev(mission), _dev(depth), _dev(features), batch_size, _stream(stream))
+
+
 def lidar_transform_device(ranges, out, count: int, stream=None) -> int:
     """tb_hip_lidar_transform_device (hip_features.h)."""
     return hip_lib().tb_hip_lidar_transform_device(_dev(ranges), _dev(out), count,
@@ -112,4 +127,5 @@ def feature_batch_error(handle) -> str:
 
 
 __all__ = ["extract_features_device", "extract_features_strided_device",
+           "extract_features_diagnostics_device", "extract_features_depth_device",
            "lidar_transform_device", "onboard_tactical_prior_device", "synchronize", "FeatureBatch", "feature_batch_error"]

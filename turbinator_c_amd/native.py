@@ -37,6 +37,10 @@ HIP_SIGNATURES = {
     "tb_hip_extract_features_strided_device":
         (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p,
                  c_size_t, c_void_p]),
+    "tb_hip_extract_features_diagnostics_device":
+        (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "tb_hip_extract_features_depth_device":
+        (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "tb_hip_lidar_transform_device": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "tb_hip_onboard_tactical_prior_device":
         (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
