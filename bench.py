@@ -224,22 +224,24 @@ def suite(torch, sets, threads: int, steps: int) -> list:
                        _events_time(torch, c5_call, max(steps // 4, 10), 3), n5, BYTES_PER_ENV))
     del dbuf, f5
 
-    # Host API, PCIe included (pageable copies, as the reference): batch 1024.
-    hb = synth.make_batch(1024, seed=9, threads=threads)
-    outh = np.empty((1024, 142), np.float32)
-    fb = features.FeatureBatch.create(0, 1024)
-    try:
-        for _ in range(3):
-            assert fb.extract_host(hb.obs, hb.mission, hb.cameras, 1024, outh) == 1
-        t0 = time.perf_counter()
-        reps = 20
-        for _ in range(reps):
-            assert fb.extract_host(hb.obs, hb.mission, hb.cameras, 1024, outh) == 1
-        per = (time.perf_counter() - t0) / reps
-    finally:
-        fb.destroy()
-    out.append(_report("host API tb_cuda_extract_features_host, 1,024 envs (PCIe-inclusive)",
-                       per, 1024, None, note="pageable host memory, synchronous"))
+    # Host API, PCIe included (pageable copies, as the reference): the
+    # trainer's default batch 32 (latency) and the 1,024 cap (bandwidth).
+    for n, reps in ((32, 200), (1024, 20)):
+        hb = synth.make_batch(n, seed=9, threads=threads)
+        outh = np.empty((n, 142), np.float32)
+        fb = features.FeatureBatch.create(0, n)
+        try:
+            for _ in range(3):
+                assert fb.extract_host(hb.obs, hb.mission, hb.cameras, n, outh) == 1
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                assert fb.extract_host(hb.obs, hb.mission, hb.cameras, n, outh) == 1
+            per = (time.perf_counter() - t0) / reps
+        finally:
+            fb.destroy()
+        out.append(_report(f"host API tb_cuda_extract_features_host, {n} envs (PCIe-inclusive)",
+                           per, n, None, note="pageable host memory, synchronous",
+                           host_GBs=round(n * (BYTES_PER_ENV - 0) / per / 1e9, 2)))
     return out
 
 

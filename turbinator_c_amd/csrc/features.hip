@@ -20,7 +20,8 @@
 //     from the CPU only by the per-bin log1p, never by summation order;
 //   * wave w also owns camera w: v_dot4_u32_u8 byte sums and a cross-lane
 //     integer reduction make the 16 quadrant means bit-exact;
-//   * wave 1 produces the 62 clamp and mission features (bit-exact).
+//   * wave 1 produces the 62 clamp and mission features (bit-exact) from
+//     values it loads together with its LiDAR and camera loads.
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -82,6 +83,22 @@ __device__ __forceinline__ float lidar_bin_feature(float r) {
     const float t = c * __builtin_amdgcn_rcpf(u);
     float f = __builtin_fmaf(l2, kLn2OverLHi, __builtin_fmaf(l2, kLn2OverLLo, t * kInvL));
     f = (x == 0.0f) ? x : f;  // log1p(+-0) = +-0
+    return valid ? f : -1.0f;
+}
+
+// The same value inside the sector sums, minus the signed-zero select: the
+// sums start at +0.0f and adding +-0 to +-0 or to a nonzero sum gives what
+// adding the exact +-0 would, so the select cannot change a sum.
+__device__ __forceinline__ float lidar_bin_term(float r) {
+    const bool valid = (r >= 0.0f) && (r < __builtin_huge_valf());
+    const float x = __builtin_fminf(r, 120.0f);
+    const float a = __builtin_fmaxf(x, 1.0f);
+    const float b = __builtin_fminf(x, 1.0f);
+    const float u = a + b;
+    const float c = b - (u - a);
+    const float l2 = __builtin_amdgcn_logf(u);
+    const float t = c * __builtin_amdgcn_rcpf(u);
+    const float f = __builtin_fmaf(l2, kLn2OverLHi, __builtin_fmaf(l2, kLn2OverLLo, t * kInvL));
     return valid ? f : -1.0f;
 }
 
@@ -243,7 +260,16 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
         const float *lidar = obs + kLidarOffset;
         float *out = rows.out + env * kFeatureDim;
 
-        // Issue every load of this wave before using any of them.
+        const float *mission =
+            reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride);
+        // Issue every load of this wave before using any of them; wave 1
+        // lanes 0..61 also fetch their proprio / scan / mission value now so
+        // no load waits behind the barrier.
+        float sv = 0.0f, m6 = 0.0f;
+        if (w == 1 && lane < 62) {
+            sv = lane < 48 ? obs[lane] : (lane < 52 ? obs[4144 + lane - 48] : mission[lane - 52]);
+            m6 = mission[6];
+        }
         f32x4 v[4];
         u32x4 px[4];
 #pragma unroll
@@ -258,10 +284,10 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             f32x4 f;
-            f.x = lidar_bin_feature(v[k].x);
-            f.y = lidar_bin_feature(v[k].y);
-            f.z = lidar_bin_feature(v[k].z);
-            f.w = lidar_bin_feature(v[k].w);
+            f.x = lidar_bin_term(v[k].x);
+            f.y = lidar_bin_term(v[k].y);
+            f.z = lidar_bin_term(v[k].z);
+            f.w = lidar_bin_term(v[k].w);
             stage[unit[k]] = f;
         }
         if constexpr (DIAG) {
@@ -321,6 +347,21 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
         } else if (lane < 4) {
             out[126 + w * 4 + lane] = 0.0f;
         }
+        if (w == 1 && lane < 62) {
+            // training.c:107-112.
+            float scalar;
+            if (lane < 48) {
+                scalar = clamp_ref(finite_or_zero(sv) / scalar_scale(lane), -1.0f, 1.0f);
+            } else if (lane < 52) {
+                scalar = clamp_ref(finite_or_zero(sv), 0.0f, 1.0f);
+            } else {
+                const int i = lane - 52;
+                const bool arena = finite_or_zero(m6) > 0.5f;
+                const float m = (i >= 7 && arena) ? 0.0f : sv;
+                scalar = clamp_ref(finite_or_zero(m), -1.0f, 1.0f);
+            }
+            out[lane] = scalar;
+        }
         if constexpr (DIAG) {
             uint32_t *diag = rows.diag + env * 224;
             if (has_cameras) {
@@ -374,24 +415,9 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
                 diag[64 + lane] = first == 0u ? 0xffffffffu : first - 1u;
                 diag[128 + lane] = count;
             }
-        } else if (w == 1 && lane < 62) {
-            // training.c:107-112.
-            float scalar;
-            if (lane < 48) {
-                scalar = clamp_ref(finite_or_zero(obs[lane]) / scalar_scale(lane), -1.0f, 1.0f);
-            } else if (lane < 52) {
-                scalar = clamp_ref(finite_or_zero(obs[4144 + lane - 48]), 0.0f, 1.0f);
-            } else {
-                const float *mission =
-                    reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride);
-                const int i = lane - 52;
-                const bool arena = finite_or_zero(mission[6]) > 0.5f;
-                const float m = (i >= 7 && arena) ? 0.0f : mission[i];
-                scalar = clamp_ref(finite_or_zero(m), -1.0f, 1.0f);
-            }
-            out[lane] = scalar;
         }
-        __syncthreads();  // the stage is reused by the next environment
+        // The stage is reused by this block's next environment, if any.
+        if (env + gridDim.x < rows.batch) __syncthreads();
     }
 }
 
