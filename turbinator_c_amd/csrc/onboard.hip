@@ -11,7 +11,8 @@
 //     minimum, cluster membership) runs one wave per environment: lane l owns
 //     rays l + 64t, so each load instruction reads 256 contiguous bytes, and
 //     the scan results are exact wave reductions (lexicographic (range, ray)
-//     minimum = first minimum in the reference scan order);
+//     minimum = first minimum in the reference scan order) done with DPP and
+//     permlane swaps rather than LDS round trips;
 //   * the scalar controller (mission decode, targets, landing / standard /
 //     inversion / BWB laws, cannon) runs in a second kernel, one thread per
 //     environment, from the scan results (register-heavy code kept apart
@@ -27,6 +28,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "turbinator/training/hip_features.h"
 
 #include "onboard_rays.inc"
@@ -37,6 +40,7 @@ constexpr int kBlockThreads = 256;
 constexpr int kWavesPerBlock = kBlockThreads / 64;
 constexpr int kRaysPerLane = 1536 / 64;    // 24
 constexpr unsigned kMaxBlocks = 1u << 20;
+constexpr unsigned kScanBlocks = 256 * 4;   // persistent scan grid: 4 per CU
 constexpr size_t kMaxBatch = 0x7fffffffu;
 constexpr float kPi = 3.14159265358979323846f;
 
@@ -93,39 +97,121 @@ __device__ __forceinline__ Attitude attitude_of(float o6, float o7, float o8, fl
     return a;
 }
 
-// Lexicographic (range, ray) minimum across the wave, carrying the world
-// offsets of the winning ray.
-__device__ __forceinline__ void wave_min_ray(float &r, int &ray, float &dx, float &dy) {
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const float r2 = __shfl_xor(r, m);
-        const int ray2 = __shfl_xor(ray, m);
-        const float dx2 = __shfl_xor(dx, m);
-        const float dy2 = __shfl_xor(dy, m);
-        const bool take = r2 < r || (r2 == r && ray2 < ray);
-        r = take ? r2 : r;
-        ray = take ? ray2 : ray;
-        dx = take ? dx2 : dx;
-        dy = take ? dy2 : dy;
-    }
+// Wave-wide reductions without the LDS crossbar: DPP exchanges inside each
+// row of 16 lanes (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror) and the gfx950 permlane swaps across rows (partner l^16, then
+// l^32).  Each step hands every lane the pair {own value, partner value};
+// the combining operations below are symmetric, so every lane ends with the
+// whole-wave result.
+template <int CTRL>
+__device__ __forceinline__ int dpp_partner(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+
+struct LaneKey {      // lexicographic (range, ray) with the winner's offsets
+    float r, dx, dy;
+    int ray;
+};
+
+__device__ __forceinline__ LaneKey key_min(const LaneKey &a, const LaneKey &b) {
+    const bool take_b = b.r < a.r || (b.r == a.r && b.ray < a.ray);
+    return take_b ? b : a;
+}
+
+template <int CTRL>
+__device__ __forceinline__ LaneKey key_partner(const LaneKey &k) {
+    LaneKey p;
+    p.r = __int_as_float(dpp_partner<CTRL>(__float_as_int(k.r)));
+    p.dx = __int_as_float(dpp_partner<CTRL>(__float_as_int(k.dx)));
+    p.dy = __int_as_float(dpp_partner<CTRL>(__float_as_int(k.dy)));
+    p.ray = dpp_partner<CTRL>(k.ray);
+    return p;
+}
+
+template <bool SWAP32>
+__device__ __forceinline__ int swap_pair(int v, int &other) {
+    const auto s = SWAP32 ? __builtin_amdgcn_permlane32_swap(v, v, false, false)
+                          : __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    other = s[1];
+    return s[0];
+}
+
+template <bool SWAP32>
+__device__ __forceinline__ LaneKey key_swap_min(const LaneKey &k) {
+    LaneKey a, b;
+    int o;
+    a.r = __int_as_float(swap_pair<SWAP32>(__float_as_int(k.r), o)); b.r = __int_as_float(o);
+    a.dx = __int_as_float(swap_pair<SWAP32>(__float_as_int(k.dx), o)); b.dx = __int_as_float(o);
+    a.dy = __int_as_float(swap_pair<SWAP32>(__float_as_int(k.dy), o)); b.dy = __int_as_float(o);
+    a.ray = swap_pair<SWAP32>(k.ray, o); b.ray = o;
+    return key_min(a, b);
+}
+
+__device__ __forceinline__ LaneKey wave_key_min(LaneKey k) {
+    k = key_min(k, key_partner<0xB1>(k));    // quad_perm [1,0,3,2]
+    k = key_min(k, key_partner<0x4E>(k));    // quad_perm [2,3,0,1]
+    k = key_min(k, key_partner<0x141>(k));   // row_half_mirror
+    k = key_min(k, key_partner<0x140>(k));   // row_mirror
+    k = key_swap_min<false>(k);              // rows 0<->1, 2<->3
+    return key_swap_min<true>(k);            // halves
 }
 
 __device__ __forceinline__ float wave_min(float v) {
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) v = fminf(v, __shfl_xor(v, m));
-    return v;
+    v = fminf(v, __int_as_float(dpp_partner<0xB1>(__float_as_int(v))));
+    v = fminf(v, __int_as_float(dpp_partner<0x4E>(__float_as_int(v))));
+    v = fminf(v, __int_as_float(dpp_partner<0x141>(__float_as_int(v))));
+    v = fminf(v, __int_as_float(dpp_partner<0x140>(__float_as_int(v))));
+    int o;
+    float a = __int_as_float(swap_pair<false>(__float_as_int(v), o));
+    v = fminf(a, __int_as_float(o));
+    a = __int_as_float(swap_pair<true>(__float_as_int(v), o));
+    return fminf(a, __int_as_float(o));
 }
 
-template <class T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
-    return v;
+__device__ __forceinline__ int wave_sum_int(int v) {
+    v += dpp_partner<0xB1>(v);
+    v += dpp_partner<0x4E>(v);
+    v += dpp_partner<0x141>(v);
+    v += dpp_partner<0x140>(v);
+    int o;
+    v = swap_pair<false>(v, o) + o;
+    return swap_pair<true>(v, o) + o;
 }
 
-// onboard_features.cuh:184-234, one wave per environment.
-__device__ void scan_lidar(const float *obs, const float ray_dir[kRaysPerLane][3], int lane,
-                           ScanResult &out) {
+__device__ __forceinline__ double wave_sum_double(double v) {
+    auto step_dpp = [](double x, auto ctrl_tag) {
+        constexpr int C = decltype(ctrl_tag)::value;
+        const long long b = __double_as_longlong(x);
+        const int lo = dpp_partner<C>((int)(b & 0xffffffffll));
+        const int hi = dpp_partner<C>((int)(b >> 32));
+        return x + __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+    };
+    v = step_dpp(v, std::integral_constant<int, 0xB1>{});
+    v = step_dpp(v, std::integral_constant<int, 0x4E>{});
+    v = step_dpp(v, std::integral_constant<int, 0x141>{});
+    v = step_dpp(v, std::integral_constant<int, 0x140>{});
+    long long b = __double_as_longlong(v);
+    int olo, ohi;
+    int lo = swap_pair<false>((int)(b & 0xffffffffll), olo);
+    int hi = swap_pair<false>((int)(b >> 32), ohi);
+    v = __longlong_as_double(((long long)hi << 32) | (unsigned)lo) +
+        __longlong_as_double(((long long)ohi << 32) | (unsigned)olo);
+    b = __double_as_longlong(v);
+    lo = swap_pair<true>((int)(b & 0xffffffffll), olo);
+    hi = swap_pair<true>((int)(b >> 32), ohi);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo) +
+           __longlong_as_double(((long long)ohi << 32) | (unsigned)olo);
+}
+
+// Ray directions as three planes (x, y, z) of 1,536 floats in LDS.
+struct RayPlanes {
+    float d[3][1536];
+};
+
+// onboard_features.cuh:184-234, one wave per environment.  Pass 1 keeps
+// each ray's corridor centre (x = +inf when the ray is outside the window or
+// the corridor), so pass 2 is a compare-and-accumulate.
+__device__ void scan_lidar(const float *obs, const RayPlanes &rays, int lane, ScanResult &out) {
     const Attitude att =
         attitude_of(ob_obs(obs[6]), ob_obs(obs[7]), ob_obs(obs[8]), ob_obs(obs[9]));
     const float *r = att.r;
@@ -134,57 +220,55 @@ __device__ void scan_lidar(const float *obs, const float ray_dir[kRaysPerLane][3
     float range[kRaysPerLane];
 #pragma unroll
     for (int t = 0; t < kRaysPerLane; ++t) {
-        const int ray = lane + 64 * t, head = ray / 768, el = (ray % 768) / 128, azi = ray % 128;
-        range[t] = ob_obs(__builtin_nontemporal_load(obs + 48 + (head * 16 + el) * 128 + azi));
+        const int head = t / 12, el = (t % 12) / 2;  // ray = lane + 64t
+        range[t] = ob_obs(__builtin_nontemporal_load(obs + 48 + (head * 16 + el) * 128 +
+                                                      (t & 1) * 64 + lane));
     }
 
-    float best_r = 30.0f, best_dx = 0.0f, best_dy = 0.0f, min_dx_c = 30.0f;
-    int best_ray = 0x7fffffff;
+    LaneKey best = {30.0f, 0.0f, 0.0f, 0x7fffffff};
+    float min_dx_c = 30.0f;
+    float xc[kRaysPerLane], yc[kRaysPerLane];
 #pragma unroll
     for (int t = 0; t < kRaysPerLane; ++t) {
         const float rg = range[t];
+        xc[t] = __builtin_huge_valf();
+        yc[t] = 0.0f;
         if (!(rg > 0.35f && rg < 11.5f)) continue;
-        const int ray = lane + 64 * t, el = (ray % 768) / 128;
-        const float dx = ray_dir[t][0], dy = ray_dir[t][1], dz = ray_dir[t][2];
+        const int ray = lane + 64 * t, el = (t % 12) / 2;
+        const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
         const float rwx = r[0] * dx + r[1] * dy + r[2] * dz;
         const float rwy = r[3] * dx + r[4] * dy + r[5] * dz;
         const float rwz = r[6] * dx + r[7] * dy + r[8] * dz;
         const float wx = rwx * rg, wy = rwy * rg, wz = rwz * rg;
-        if (el < 4 && rg < best_r) { best_r = rg; best_dx = wx; best_dy = wy; best_ray = ray; }
+        if (el < 4 && rg < best.r) { best.r = rg; best.dx = wx; best.dy = wy; best.ray = ray; }
         const float x_center = wx + rwx * 1.10f;
         const float y_center = py + wy + rwy * 1.10f;
         if (fabsf(wz) <= 2.1f && x_center >= -0.35f && x_center <= 10.5f &&
-            fabsf(y_center) <= 3.5f && x_center < min_dx_c)
-            min_dx_c = x_center;
+            fabsf(y_center) <= 3.5f) {
+            xc[t] = x_center;
+            yc[t] = y_center;
+            min_dx_c = fminf(min_dx_c, x_center);
+        }
     }
-    wave_min_ray(best_r, best_ray, best_dx, best_dy);
+    best = wave_key_min(best);
     min_dx_c = wave_min(min_dx_c);
 
+    const float limit = min_dx_c + 1.4f;
     int count = 0;
     double y_sum = 0.0;
 #pragma unroll
     for (int t = 0; t < kRaysPerLane; ++t) {
-        const float rg = range[t];
-        if (!(rg > 0.35f && rg < 11.5f)) continue;
-        const float dx = ray_dir[t][0], dy = ray_dir[t][1], dz = ray_dir[t][2];
-        const float rwx = r[0] * dx + r[1] * dy + r[2] * dz;
-        const float rwy = r[3] * dx + r[4] * dy + r[5] * dz;
-        const float rwz = r[6] * dx + r[7] * dy + r[8] * dz;
-        const float wx = rwx * rg, wy = rwy * rg, wz = rwz * rg;
-        const float x_center = wx + rwx * 1.10f;
-        const float y_center = py + wy + rwy * 1.10f;
-        if (fabsf(wz) <= 2.1f && x_center >= -0.35f && x_center <= 10.5f &&
-            fabsf(y_center) <= 3.5f && x_center <= min_dx_c + 1.4f) {
+        if (xc[t] <= limit) {
             ++count;
-            y_sum += (double)y_center;
+            y_sum += (double)yc[t];
         }
     }
-    count = wave_sum(count);
-    y_sum = wave_sum(y_sum);
-    out.min_r = best_r;
-    out.min_r_dx = best_dx;
-    out.min_r_dy = best_dy;
-    out.min_ray = best_ray == 0x7fffffff ? -1 : best_ray;
+    count = wave_sum_int(count);
+    y_sum = wave_sum_double(y_sum);
+    out.min_r = best.r;
+    out.min_r_dx = best.dx;
+    out.min_r_dy = best.dy;
+    out.min_ray = best.ray == 0x7fffffff ? -1 : best.ray;
     out.min_dx_c = min_dx_c;
     out.cluster_count = count;
     out.cluster_y_sum = (float)y_sum;
@@ -667,22 +751,25 @@ struct OnboardRows {
     size_t batch;
 };
 
-// Phase 1: one wave per environment scans the LiDAR.  The 32-byte result is
+// Phase 1: one wave per environment scans the LiDAR (persistent blocks share
+// one LDS copy of the ray table).  The 32-byte result is
 // parked in the environment's own prior row (60 bytes), which phase 2 reads
 // before it writes the 15 prior values there: no scratch memory is needed.
 __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows rows) {
+    __shared__ RayPlanes rays;
+    for (int i = threadIdx.x; i < 1536; i += kBlockThreads) {
+        rays.d[0][i] = kRayDir[i * 3 + 0];
+        rays.d[1][i] = kRayDir[i * 3 + 1];
+        rays.d[2][i] = kRayDir[i * 3 + 2];
+    }
+    __syncthreads();
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float ray_dir[kRaysPerLane][3];
-#pragma unroll
-    for (int t = 0; t < kRaysPerLane; ++t)
-#pragma unroll
-        for (int c = 0; c < 3; ++c) ray_dir[t][c] = kRayDir[(lane + 64 * t) * 3 + c];
     for (size_t env = (size_t)blockIdx.x * kWavesPerBlock + w; env < rows.batch;
          env += (size_t)gridDim.x * kWavesPerBlock) {
         const float *obs = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
         ScanResult s;
-        scan_lidar(obs, ray_dir, lane, s);
+        scan_lidar(obs, rays, lane, s);
         if (lane == 0) {
             float *park = rows.prior + env * 15;
             park[0] = s.min_r;
@@ -743,10 +830,10 @@ extern "C" int tb_hip_onboard_tactical_prior_device(const float *obs, const floa
     rows.batch = batch_size;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const size_t scan_want = (batch_size + kWavesPerBlock - 1) / kWavesPerBlock;
+    const unsigned scan_blocks = scan_want > kScanBlocks ? kScanBlocks : (unsigned)scan_want;
     const size_t ctrl_want = (batch_size + kBlockThreads - 1) / kBlockThreads;
     (void)hipGetLastError();
-    onboard_scan_kernel<<<scan_want > kMaxBlocks ? kMaxBlocks : (unsigned)scan_want,
-                          kBlockThreads, 0, s>>>(rows);
+    onboard_scan_kernel<<<scan_blocks, kBlockThreads, 0, s>>>(rows);
     onboard_control_kernel<<<ctrl_want > kMaxBlocks ? kMaxBlocks : (unsigned)ctrl_want,
                              kBlockThreads, 0, s>>>(rows);
     return hipGetLastError() == hipSuccess;
