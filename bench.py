@@ -224,6 +224,37 @@ def suite(torch, sets, threads: int, steps: int) -> list:
                        _events_time(torch, c5_call, max(steps // 4, 10), 3), n5, BYTES_PER_ENV))
     del dbuf, f5
 
+    # Replay sampling (f1): 16,384 samples from a 65,536-slot SoA replay, fused
+    # versus the reference's gather-into-a-batch followed by extraction.
+    cap = 65536
+    rep = synth.make_batch(cap, seed=5, threads=threads)
+    r_obs = torch.from_numpy(rep.obs).cuda()
+    r_mis = torch.from_numpy(rep.mission).cuda()
+    r_cam = torch.from_numpy(rep.cameras).cuda()
+    del rep
+    idx = torch.randint(0, cap, (BATCH,), dtype=torch.int32, device="cuda")
+    fo = torch.empty((BATCH, 142), dtype=torch.float32, device="cuda")
+
+    def fused_call(i, s):
+        assert features.extract_features_indexed_device(r_obs, OBS_B, r_mis, MISSION_B, r_cam,
+                                                        CAMERA_B, cap, idx, fo, BATCH, s) == 1
+    out.append(_report("replay sample 16,384 of 65,536 + features, fused",
+                       _events_time(torch, fused_call, steps, 5), BATCH, BYTES_PER_ENV))
+    g_obs = torch.empty((BATCH, 4148), dtype=torch.float32, device="cuda")
+    g_mis = torch.empty((BATCH, 10), dtype=torch.float32, device="cuda")
+    g_cam = torch.empty((BATCH, 16384), dtype=torch.uint8, device="cuda")
+    lidx = idx.long()
+
+    def gather_call(i, s):
+        torch.index_select(r_obs, 0, lidx, out=g_obs)
+        torch.index_select(r_mis, 0, lidx, out=g_mis)
+        torch.index_select(r_cam, 0, lidx, out=g_cam)
+        assert features.extract_features_device(g_obs, g_mis, g_cam, fo, BATCH, s) == 1
+    out.append(_report("replay sample 16,384 of 65,536: gather batch, then features",
+                       _events_time(torch, gather_call, steps, 5), BATCH, BYTES_PER_ENV,
+                       note="bytes_per_env counts only the fused minimum"))
+    del r_obs, r_mis, r_cam, g_obs, g_mis, g_cam
+
     # Host API, PCIe included (pageable copies, as the reference): the
     # trainer's default batch 32 (latency) and the 1,024 cap (bandwidth).
     for n, reps in ((32, 200), (1024, 20)):

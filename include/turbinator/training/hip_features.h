@@ -41,6 +41,23 @@ int tb_hip_extract_features_strided_device(const void *obs, size_t obs_stride,
                                            float *features,
                                            size_t batch_size, void *stream);
 
+/* Fused replay sampling + features: output row e holds the 142 features of
+ * input row indices[e], read in place from storage laid out like the
+ * strided entry's (byte strides; e.g. the SoA replay fields of
+ * src/gpu/replay.cu:27-48 with strides 16,592 / 40 / 16,384, or 66,672-byte
+ * transition records).  This replaces the reference's gather of every
+ * sampled field into a batch followed by feature extraction
+ * (replay.cu:130-187 then features.cu:158-169) with one pass that reads
+ * only the sampled observation bytes.  indices are device uint32 with
+ * values < capacity; an output row whose index is >= capacity reads nothing
+ * and is filled with NaN.  Same argument rules as the strided entry, plus
+ * NULL indices or capacity 0 -> 0. */
+int tb_hip_extract_features_indexed_device(const void *obs, size_t obs_stride,
+                                           const void *mission, size_t mission_stride,
+                                           const void *cameras, size_t camera_stride,
+                                           size_t capacity, const unsigned int *indices,
+                                           float *features, size_t batch_size, void *stream);
+
 /* The 142 features of tb_cuda_extract_features_device plus, from the same
  * single pass, per-environment diagnostics that have no counterpart in the
  * reference feature vector (training.c:107-141).  `diagnostics` receives

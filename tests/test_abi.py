@@ -68,6 +68,10 @@ def test_argument_validation_without_gpu():
                                                       dummy, 1, None) == 0
     assert lib.tb_hip_extract_features_strided_device(ctypes.c_void_p(18), 16592, dummy, 40,
                                                       None, 0, dummy, 1, None) == 0
+    assert lib.tb_hip_extract_features_indexed_device(dummy, 16592, dummy, 40, None, 0, 8, None,
+                                                      dummy, 1, None) == 0
+    assert lib.tb_hip_extract_features_indexed_device(dummy, 16592, dummy, 40, None, 0, 0, dummy,
+                                                      dummy, 1, None) == 0
     assert lib.tb_hip_lidar_transform_device(None, dummy, 1, None) == 0
     assert lib.tb_hip_lidar_transform_device(dummy, dummy, 0, None) == 0
     # Host object: max_batch 0 or above 1024 -> NULL before any device call.

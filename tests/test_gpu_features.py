@@ -304,3 +304,66 @@ def test_depth_cameras_special_values(torch_cuda, hip):
     got = run_depth(torch_cuda, hip, b.obs, b.mission, depth)
     want = oracle.features(b.obs, b.mission, oracle.depth_to_luma(depth))
     assert_feature_parity(got, want, "depth-special")
+
+
+def reference_sampler(seed: int, count: int, size: int) -> np.ndarray:
+    """Index stream of the reference replay (src/gpu/replay.cu:18-25,153):
+    xorshift64* modulo the current size."""
+    state, out = seed or 1, np.empty(count, np.uint32)
+    mask = (1 << 64) - 1
+    for i in range(count):
+        x = state
+        x ^= x >> 12
+        x ^= (x << 25) & mask
+        x ^= x >> 27
+        state = x
+        out[i] = ((x * 2685821657736338717) & mask) % size
+    return out
+
+
+def test_indexed_soa_replay(torch_cuda, hip):
+    note("fused replay sampling: SoA storage, 4096 slots, 2048 samples")
+    torch = torch_cuda
+    cap, n = 4096, 2048
+    b = synth.make_batch(cap, seed=31, threads=16)
+    idx = reference_sampler(42, n, cap)
+    idx[::97] = cap + 5                      # out-of-range rows -> NaN, nothing read
+    d_obs, d_mis = torch.from_numpy(b.obs).cuda(), torch.from_numpy(b.mission).cuda()
+    d_cam = torch.from_numpy(b.cameras).cuda()
+    d_idx = torch.from_numpy(idx.view(np.int32)).cuda()
+    out = torch.zeros((n, 142), dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    assert hip.extract_features_indexed_device(d_obs, 16592, d_mis, 40, d_cam, 16384, cap, d_idx,
+                                               out, n, s) == 1
+    assert hip.synchronize(s) == 1
+    got = out.cpu().numpy()
+    bad = idx >= cap
+    assert np.all(np.isnan(got[bad]))
+    ok = ~bad
+    want = oracle.features(b.obs[idx[ok]], b.mission[idx[ok]], b.cameras[idx[ok]])
+    assert_feature_parity(got[ok], want, "indexed-soa")
+
+
+def test_indexed_aos_records(torch_cuda, hip):
+    note("fused replay sampling: 66,672-byte records, next_obs fields")
+    torch = torch_cuda
+    cap, n = 1024, 700
+    buf = np.zeros(cap * RECORD, np.uint8)
+    synth.fill_records(buf, cap, RECORD, OFF_NEXT_OBS, OFF_NEXT_MISSION, OFF_NEXT_CAM, seed=9,
+                       threads=16)
+    idx = reference_sampler(7, n, cap)
+    full = oracle.features_strided(buf, cap, RECORD, OFF_NEXT_OBS, OFF_NEXT_MISSION,
+                                   OFF_NEXT_CAM, threads=16)
+    d = torch.from_numpy(buf).cuda()
+    base = d.data_ptr()
+    d_idx = torch.from_numpy(idx.view(np.int32)).cuda()
+    out = torch.zeros((n, 142), dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    assert hip.extract_features_indexed_device(base + OFF_NEXT_OBS, RECORD,
+                                               base + OFF_NEXT_MISSION, RECORD,
+                                               base + OFF_NEXT_CAM, RECORD, cap, d_idx, out, n,
+                                               s) == 1
+    assert hip.synchronize(s) == 1
+    assert_feature_parity(out.cpu().numpy(), full[idx], "indexed-aos")

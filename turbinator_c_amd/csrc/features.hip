@@ -64,6 +64,8 @@ struct Rows {
     size_t depth_stride;
     float *out;
     uint32_t *diag;  // optional [batch, 224] diagnostics words (DIAG kernels)
+    const uint32_t *index;  // optional: output row e reads input row index[e]
+    size_t capacity;        // input rows available when index is set
     size_t batch;
 };
 
@@ -256,12 +258,19 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
     }
 
     for (size_t env = blockIdx.x; env < rows.batch; env += gridDim.x) {
-        const float *obs = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
-        const float *lidar = obs + kLidarOffset;
         float *out = rows.out + env * kFeatureDim;
-
+        size_t src = env;
+        if (rows.index) {
+            src = rows.index[env];
+            if (src >= rows.capacity) {  // reads nothing; marks the row
+                if (threadIdx.x < kFeatureDim) out[threadIdx.x] = __builtin_nanf("");
+                continue;
+            }
+        }
+        const float *obs = reinterpret_cast<const float *>(rows.obs + src * rows.obs_stride);
+        const float *lidar = obs + kLidarOffset;
         const float *mission =
-            reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride);
+            reinterpret_cast<const float *>(rows.mission + src * rows.mission_stride);
         // Issue every load of this wave before using any of them; wave 1
         // lanes 0..61 also fetch their proprio / scan / mission value now so
         // no load waits behind the barrier.
@@ -276,7 +285,7 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
         for (int k = 0; k < 4; ++k) v[k] = load_lidar4<LV>(lidar + (4 * w + k) * 256 + 4 * lane);
         if (!DEPTH && has_cameras) {
             // Camera w, rows 16k + lane/4, bytes 16*(lane%4)..+15.
-            const unsigned char *cam = rows.cameras + env * rows.camera_stride + w * 4096;
+            const unsigned char *cam = rows.cameras + src * rows.camera_stride + w * 4096;
 #pragma unroll
             for (int k = 0; k < 4; ++k) px[k] = load_camera16<CV>(cam + (k * 64 + lane) * 16);
         }
@@ -317,7 +326,7 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
             // Camera w as 4096 floats: load k covers rows 4k + lane/16,
             // columns 4*(lane%16)..+3, so qy = k/8 and qx = lane bit 3.
             const float *cam = reinterpret_cast<const float *>(
-                reinterpret_cast<const unsigned char *>(rows.depth) + env * rows.depth_stride) +
+                reinterpret_cast<const unsigned char *>(rows.depth) + src * rows.depth_stride) +
                 w * 4096;
             unsigned top = 0u, bottom = 0u;
 #pragma unroll
@@ -497,6 +506,8 @@ extern "C" int tb_cuda_extract_features_device(const float *device_obs,
     rows.depth_stride = 0;
     rows.out = device_features;
     rows.diag = nullptr;
+    rows.index = nullptr;
+    rows.capacity = 0;
     rows.batch = batch_size;
     return launch_features(rows, reinterpret_cast<hipStream_t>(stream));
 }
@@ -519,16 +530,17 @@ extern "C" int tb_hip_extract_features_diagnostics_device(const float *obs, cons
     rows.depth_stride = 0;
     rows.out = features;
     rows.diag = static_cast<uint32_t *>(diagnostics);
+    rows.index = nullptr;
+    rows.capacity = 0;
     rows.batch = batch_size;
     return launch_features(rows, reinterpret_cast<hipStream_t>(stream));
 }
 
-extern "C" int tb_hip_extract_features_strided_device(const void *obs, size_t obs_stride,
-                                                      const void *mission,
-                                                      size_t mission_stride,
-                                                      const void *cameras,
-                                                      size_t camera_stride, float *features,
-                                                      size_t batch_size, void *stream) {
+namespace {
+
+int strided_entry(const void *obs, size_t obs_stride, const void *mission, size_t mission_stride,
+                  const void *cameras, size_t camera_stride, const uint32_t *index,
+                  size_t capacity, float *features, size_t batch_size, void *stream) {
     if (!obs || !mission || !features || batch_size == 0 || batch_size > kMaxBatch) return 0;
     if (((reinterpret_cast<uintptr_t>(obs) | obs_stride) & 3u) != 0 ||
         ((reinterpret_cast<uintptr_t>(mission) | mission_stride) & 3u) != 0 ||
@@ -545,8 +557,31 @@ extern "C" int tb_hip_extract_features_strided_device(const void *obs, size_t ob
     rows.depth_stride = 0;
     rows.out = features;
     rows.diag = nullptr;
+    rows.index = index;
+    rows.capacity = capacity;
     rows.batch = batch_size;
     return launch_features(rows, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" int tb_hip_extract_features_strided_device(const void *obs, size_t obs_stride,
+                                                      const void *mission,
+                                                      size_t mission_stride,
+                                                      const void *cameras,
+                                                      size_t camera_stride, float *features,
+                                                      size_t batch_size, void *stream) {
+    return strided_entry(obs, obs_stride, mission, mission_stride, cameras, camera_stride,
+                         nullptr, 0, features, batch_size, stream);
+}
+
+extern "C" int tb_hip_extract_features_indexed_device(
+    const void *obs, size_t obs_stride, const void *mission, size_t mission_stride,
+    const void *cameras, size_t camera_stride, size_t capacity, const unsigned int *indices,
+    float *features, size_t batch_size, void *stream) {
+    if (!indices || capacity == 0) return 0;
+    return strided_entry(obs, obs_stride, mission, mission_stride, cameras, camera_stride,
+                         indices, capacity, features, batch_size, stream);
 }
 
 extern "C" int tb_hip_extract_features_depth_device(const float *obs, const float *mission,
@@ -566,6 +601,8 @@ extern "C" int tb_hip_extract_features_depth_device(const float *obs, const floa
     rows.depth_stride = 16384 * sizeof(float);
     rows.out = features;
     rows.diag = nullptr;
+    rows.index = nullptr;
+    rows.capacity = 0;
     rows.batch = batch_size;
     return launch_features(rows, reinterpret_cast<hipStream_t>(stream));
 }

@@ -46,6 +46,15 @@ def extract_features_strided_device(obs, obs_stride: int, mission, mission_strid
         _dev(features), batch_size, _stream(stream))
 
 
+def extract_features_indexed_device(obs, obs_stride: int, mission, mission_stride: int,
+                                    cameras, camera_stride: int, capacity: int, indices,
+                                    features, batch_size: int, stream=None) -> int:
+    """tb_hip_extract_features_indexed_device (hip_features.h)."""
+    return hip_lib().tb_hip_extract_features_indexed_device(
+        _dev(obs), obs_stride, _dev(mission), mission_stride, _dev(cameras), camera_stride,
+        capacity, _dev(indices), _dev(features), batch_size, _stream(stream))
+
+
 def extract_features_diagnostics_device(obs, mission, cameras, features, diagnostics,
                                         batch_size: int, stream=None) -> int:
     """tb_hip_extract_features_diagnostics_device (hip_features.h)."""
@@ -127,5 +136,5 @@ def feature_batch_error(handle) -> str:
 
 
 __all__ = ["extract_features_device", "extract_features_strided_device",
-           "extract_features_diagnostics_device", "extract_features_depth_device",
+           "extract_features_diagnostics_device", "extract_features_indexed_device", "extract_features_depth_device",
            "lidar_transform_device", "onboard_tactical_prior_device", "synchronize", "FeatureBatch", "feature_batch_error"]

@@ -37,6 +37,9 @@ HIP_SIGNATURES = {
     "tb_hip_extract_features_strided_device":
         (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t, c_void_p,
                  c_size_t, c_void_p]),
+    "tb_hip_extract_features_indexed_device":
+        (c_int, [c_void_p, c_size_t, c_void_p, c_size_t, c_void_p, c_size_t, c_size_t, c_void_p,
+                 c_void_p, c_size_t, c_void_p]),
     "tb_hip_extract_features_diagnostics_device":
         (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "tb_hip_extract_features_depth_device":
