@@ -208,6 +208,24 @@ def suite(torch, sets, threads: int, steps: int) -> list:
     out.append(_report("onboard tactical+prior (16,384 envs)",
                        _events_time(torch, onboard_call, steps, 5), BATCH, None))
 
+    # f3: the 618M actor's sensor preparation (network_gpu.cu:1446-1451) fused:
+    # proprio 91 + mission 49 + tactical 24 + prior 15 + 6x16x128 LiDAR
+    # channels + 4x64x64 luma per environment.
+    a_pro = torch.empty((BATCH, 91), dtype=torch.float32, device="cuda")
+    a_mis = torch.empty((BATCH, 49), dtype=torch.float32, device="cuda")
+    a_lid = torch.empty((BATCH, 6, 16, 128), dtype=torch.float32, device="cuda")
+    a_lum = torch.empty((BATCH, 4, 64, 64), dtype=torch.float32, device="cuda")
+
+    def actor_call(i, s):
+        o, m, c, _ = sets[i % len(sets)]
+        assert features.actor_inputs_device(o, m, c, a_pro, a_mis, tac, pri, a_lid, a_lum,
+                                            BATCH, s) == 1
+    actor_bytes = OBS_B + MISSION_B + CAMERA_B + 4 * (91 + 49 + 24 + 15 + 6 * 2048 + 16384)
+    out.append(_report("618M actor sensor preparation, fused (16,384 envs)",
+                       _events_time(torch, actor_call, steps, 5), BATCH, actor_bytes,
+                       note="bytes_per_env: inputs once + every output once"))
+    del a_pro, a_mis, a_lid, a_lum
+
     # Configuration 5: 65,536 replay records of 66,672 B, features in place.
     n5, rec = 65536, 66672
     buf = np.zeros(n5 * rec, np.uint8)

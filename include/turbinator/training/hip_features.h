@@ -111,6 +111,25 @@ int tb_hip_onboard_tactical_prior_device(const float *obs, const float *mission,
                                          float *tactical, float *prior, float *diag,
                                          size_t batch_size, void *stream);
 
+/* The 618M actor's sensor preparation in one call, replacing the reference
+ * kernels scalar_inputs, lidar_channels and camera_luma
+ * (src/network/network_gpu.cu:274-304, 467-483; launched at :1446-1451).
+ * Device pointers, row-major per environment:
+ *   proprio      [batch, 91]  52 symlog scalars, tactical[24], prior[15]
+ *   mission_vec  [batch, 49]  10 finite mission values, tactical, prior
+ *   tactical     [batch, 24], prior [batch, 15]
+ *   lidar_channels [batch, 6, 16, 128] (nullable): inverse range, range/30
+ *                and validity of head c%2 for channel c
+ *   camera_luma  [batch, 16384] (nullable): byte / 255 - 0.5
+ * obs, cameras, lidar_channels and camera_luma must be 16-byte aligned;
+ * camera_luma needs cameras.  Returns 0 for NULL required pointers,
+ * misalignment, batch 0 or above 0x7fffffff. */
+int tb_hip_actor_inputs_device(const float *obs, const float *mission,
+                               const unsigned char *cameras, float *proprio,
+                               float *mission_vec, float *tactical, float *prior,
+                               float *lidar_channels, float *camera_luma,
+                               size_t batch_size, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -46,6 +46,8 @@ def lib() -> ctypes.CDLL:
         l.orc_diagnostics_env.restype = None
         l.orc_onboard_env.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]
         l.orc_onboard_env.restype = None
+        l.orc_actor_inputs_env.argtypes = [c_void_p] * 9
+        l.orc_actor_inputs_env.restype = None
         l.orc_onboard_ray_dir.argtypes = [c_int, c_void_p]
         l.orc_onboard_ray_dir.restype = None
         _orc = l
@@ -125,6 +127,25 @@ def onboard(obs: np.ndarray, mission: np.ndarray):
                               np.ascontiguousarray(mission[e], np.float32).ctypes.data,
                               tac[e].ctypes.data, pri[e].ctypes.data, diag[e].ctypes.data)
     return tac, pri, diag
+
+
+def actor_inputs(obs: np.ndarray, mission: np.ndarray, cameras: np.ndarray | None) -> dict:
+    """The 618M actor's prepared inputs per environment (dict of arrays)."""
+    b = obs.shape[0]
+    out = {"proprio": np.empty((b, 91), np.float32), "mission": np.empty((b, 49), np.float32),
+           "tactical": np.empty((b, 24), np.float32), "prior": np.empty((b, 15), np.float32),
+           "lidar": np.empty((b, 6, 16, 128), np.float32),
+           "luma": None if cameras is None else np.empty((b, 4, 64, 64), np.float32)}
+    for e in range(b):
+        cam = None if cameras is None else np.ascontiguousarray(cameras[e]).ctypes.data
+        lib().orc_actor_inputs_env(
+            np.ascontiguousarray(obs[e], np.float32).ctypes.data,
+            np.ascontiguousarray(mission[e], np.float32).ctypes.data, cam,
+            out["proprio"][e].ctypes.data, out["mission"][e].ctypes.data,
+            out["tactical"][e].ctypes.data, out["prior"][e].ctypes.data,
+            out["lidar"][e].ctypes.data,
+            None if out["luma"] is None else out["luma"][e].ctypes.data)
+    return out
 
 
 def onboard_ray_table() -> np.ndarray:

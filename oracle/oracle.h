@@ -58,6 +58,13 @@ void orc_diagnostics_env(const float *obs, const uint8_t *cameras, uint32_t *dia
 void orc_onboard_env(const float *obs, const float *mission,
                      float *tactical24, float *prior15, float *diag4);
 
+/* The 618M actor's sensor preparation (network_gpu.cu:274-304,467-483):
+ * proprio[91], mission_vec[49], tactical[24], prior[15], lidar[6*2048]
+ * (nullable), luma[16384] (nullable; needs cameras). */
+void orc_actor_inputs_env(const float *obs, const float *mission, const uint8_t *cameras,
+                          float *proprio, float *mission_vec, float *tactical, float *prior,
+                          float *lidar, float *luma);
+
 /* Body-frame direction of onboard ray head*768 + el*128 + azi. */
 void orc_onboard_ray_dir(int ray, float *xyz);
 

@@ -72,6 +72,13 @@ def test_argument_validation_without_gpu():
                                                       dummy, 1, None) == 0
     assert lib.tb_hip_extract_features_indexed_device(dummy, 16592, dummy, 40, None, 0, 0, dummy,
                                                       dummy, 1, None) == 0
+    odd = ctypes.c_void_p(20)
+    assert lib.tb_hip_actor_inputs_device(None, dummy, dummy, dummy, dummy, dummy, dummy, dummy,
+                                          dummy, 1, None) == 0
+    assert lib.tb_hip_actor_inputs_device(dummy, dummy, None, dummy, dummy, dummy, dummy, dummy,
+                                          dummy, 1, None) == 0
+    assert lib.tb_hip_actor_inputs_device(odd, dummy, dummy, dummy, dummy, dummy, dummy, dummy,
+                                          dummy, 1, None) == 0
     assert lib.tb_hip_lidar_transform_device(None, dummy, 1, None) == 0
     assert lib.tb_hip_lidar_transform_device(dummy, dummy, 0, None) == 0
     # Host object: max_batch 0 or above 1024 -> NULL before any device call.

@@ -1,0 +1,168 @@
+"""GPU parity of the 618M actor's fused sensor preparation, through the
+C-ABI entry tb_hip_actor_inputs_device, against the CPU oracle
+(oracle/actor_inputs_oracle.c, restating network_gpu.cu:274-304, 467-483).
+
+Classes:
+  * LiDAR channels, camera luma and mission_vec[0..9]: bit-exact;
+  * the 52 symlog scalars: |gpu - cpu| <= 1e-5 |cpu| + 1e-6 (log1p is this
+    backend's own evaluation, as in the LiDAR feature means);
+  * tactical / prior: 5e-5 absolute and the same NaN pattern (the onboard
+    tolerance); their copies in proprio / mission_vec equal the GPU's own
+    tactical / prior bit-for-bit.
+At the 16,384-environment configuration the channels and luma are checked
+against numpy closed forms for every environment and the rest against the
+oracle on a sample of environments.
+"""
+from __future__ import annotations
+
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.test_actor_inputs_oracle import exact_luma, numpy_lidar_channels, ulp_distance
+from turbinator_c_amd import synth
+
+pytestmark = pytest.mark.gpu
+H2_TOL = 5e-5
+
+
+def note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def u32(a):
+    return np.ascontiguousarray(a).view(np.uint32)
+
+
+def run_actor(torch, hip, obs, mission, cameras, lidar=True, luma=True):
+    b = obs.shape[0]
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()   # noqa: E731
+    nan = lambda *shape: torch.full(shape, float("nan"), dtype=torch.float32,  # noqa: E731
+                                    device="cuda")
+    d_obs, d_mis = dev(obs), dev(mission)
+    d_cam = None if cameras is None else dev(cameras)
+    out = {"proprio": nan(b, 91), "mission": nan(b, 49), "tactical": nan(b, 24),
+           "prior": nan(b, 15), "lidar": nan(b, 6, 16, 128) if lidar else None,
+           "luma": nan(b, 4, 64, 64) if luma else None}
+    s = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    assert hip.actor_inputs_device(d_obs, d_mis, d_cam, out["proprio"], out["mission"],
+                                   out["tactical"], out["prior"], out["lidar"], out["luma"],
+                                   b, s) == 1
+    assert hip.synchronize(s) == 1
+    return {k: None if v is None else v.cpu().numpy() for k, v in out.items()}
+
+
+def check_h2(got, want, label):
+    for name in ("tactical", "prior"):
+        g, w = got[name], want[name]
+        assert np.array_equal(np.isnan(g), np.isnan(w)), f"{label}: {name} NaN pattern"
+        d = np.abs(np.nan_to_num(g) - np.nan_to_num(w))
+        assert d.max() <= H2_TOL, f"{label}: {name} {np.argwhere(d > H2_TOL)[:3]}"
+
+
+def check_copies(got, label):
+    assert np.array_equal(u32(got["proprio"][:, 52:76]), u32(got["tactical"])), label
+    assert np.array_equal(u32(got["proprio"][:, 76:91]), u32(got["prior"])), label
+    assert np.array_equal(u32(got["mission"][:, 10:34]), u32(got["tactical"])), label
+    assert np.array_equal(u32(got["mission"][:, 34:49]), u32(got["prior"])), label
+
+
+def check_symlog(got, want, label) -> int:
+    g, w = got[:, :52].astype(np.float64), want[:, :52].astype(np.float64)
+    bad = np.abs(g - w) > 1e-5 * np.abs(w) + 1e-6
+    assert not bad.any(), f"{label}: symlog {np.argwhere(bad)[:3]}"
+    return int(ulp_distance(got[:, :52], want[:, :52]).max())
+
+
+def finite_scalars(b):
+    """Variant SPECIAL with its 3e38 scalars replaced: huge finite inputs make
+    the onboard controller ill-conditioned (covered in test_gpu_onboard)."""
+    obs, mission = b.obs.copy(), b.mission.copy()
+    for sl in (np.s_[:, :48], np.s_[:, 4144:]):
+        v = obs[sl]
+        v[np.abs(v) == np.float32(3e38)] = np.float32(7.5)
+        obs[sl] = v
+    mission[np.abs(mission) == np.float32(3e38)] = np.float32(0.25)
+    return obs, mission
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5])
+def test_variants_against_oracle(torch_cuda, hip, variant):
+    note(f"actor inputs variant {variant}, 256 envs")
+    b = synth.make_batch(256, seed=600 + variant, variant=variant, threads=16)
+    obs, mission = finite_scalars(b)
+    got = run_actor(torch_cuda, hip, obs, mission, b.cameras)
+    want = oracle.actor_inputs(obs, mission, b.cameras)
+    assert np.array_equal(u32(got["lidar"]), u32(want["lidar"])), "lidar channels"
+    assert np.array_equal(u32(got["luma"]), u32(want["luma"])), "luma"
+    assert np.array_equal(u32(got["mission"][:, :10]), u32(want["mission"][:, :10]))
+    ulps = check_symlog(got["proprio"], want["proprio"], f"variant{variant}")
+    check_h2(got, want, f"variant{variant}")
+    check_copies(got, f"variant{variant}")
+    note(f"variant {variant}: symlog max {ulps} ulp")
+
+
+def test_symlog_dense_sweep(torch_cuda, hip):
+    """Every scalar slot over magnitudes 1e-30 .. 1e3 (both signs), zeros,
+    and non-finite values."""
+    note("actor inputs symlog sweep")
+    vals = np.concatenate([np.logspace(-30, 3, 3000).astype(np.float32), [0, -0.0, np.nan,
+                                                                           np.inf, -np.inf]])
+    vals = np.concatenate([vals, -vals]).astype(np.float32)
+    n = (vals.size + 51) // 52
+    flat = np.resize(vals, n * 52).reshape(n, 52)
+    obs = np.zeros((n, 4148), np.float32)
+    obs[:, :48] = flat[:, :48]
+    obs[:, 4144:] = flat[:, 48:]
+    mission = np.zeros((n, 10), np.float32)
+    got = run_actor(torch_cuda, hip, obs, mission, None, lidar=False, luma=False)
+    want = oracle.actor_inputs(obs, mission, None)
+    ulps = check_symlog(got["proprio"], want["proprio"], "sweep")
+    note(f"symlog sweep: max {ulps} ulp over {n * 52} values")
+
+
+def test_optional_outputs_and_ragged(torch_cuda, hip):
+    note("actor inputs without lidar/luma outputs, batches 1 and 3")
+    for n in (1, 3):
+        b = synth.make_batch(n, seed=650 + n)
+        got = run_actor(torch_cuda, hip, b.obs, b.mission, None, lidar=False, luma=False)
+        want = oracle.actor_inputs(b.obs, b.mission, None)
+        check_symlog(got["proprio"], want["proprio"], f"ragged{n}")
+        check_h2(got, want, f"ragged{n}")
+        check_copies(got, f"ragged{n}")
+
+
+def test_config_16384(torch_cuda, hip):
+    """BASELINE's 16,384-environment batch: channels and luma bit-exact for
+    every environment against numpy; the rest against the oracle on 512
+    sampled environments."""
+    note("actor inputs 16384 envs")
+    b = synth.make_batch(16384, seed=1, variant=synth.EDGE_QUARTERS, threads=16)
+    got = run_actor(torch_cuda, hip, b.obs, b.mission, b.cameras)
+    assert np.array_equal(u32(got["lidar"]), u32(numpy_lidar_channels(b.obs)))
+    assert np.array_equal(u32(got["luma"]), u32(exact_luma(b.cameras)))
+    check_copies(got, "16384")
+    pick = np.random.default_rng(5).choice(16384, 512, replace=False)
+    want = oracle.actor_inputs(b.obs[pick], b.mission[pick], b.cameras[pick])
+    sub = {k: got[k][pick] for k in ("proprio", "mission", "tactical", "prior")}
+    check_symlog(sub["proprio"], want["proprio"], "16384")
+    assert np.array_equal(u32(sub["mission"][:, :10]), u32(want["mission"][:, :10]))
+    check_h2(sub, want, "16384")
+
+
+def test_argument_validation(hip):
+    lib = hip.hip_lib()
+    d = ctypes.c_void_p(256)
+    odd = ctypes.c_void_p(260)
+    f = lib.tb_hip_actor_inputs_device
+    assert f(None, d, d, d, d, d, d, d, d, 1, None) == 0          # obs NULL
+    assert f(d, d, d, None, d, d, d, d, d, 1, None) == 0          # proprio NULL
+    assert f(d, d, None, d, d, d, d, d, d, 1, None) == 0          # luma without cameras
+    assert f(odd, d, d, d, d, d, d, d, d, 1, None) == 0           # misaligned obs
+    assert f(d, d, d, d, d, d, d, odd, d, 1, None) == 0           # misaligned channels
+    assert f(d, d, d, d, d, d, d, d, d, 0, None) == 0             # empty batch

@@ -38,6 +38,7 @@ namespace {
 
 constexpr int kBlockThreads = 256;
 constexpr int kWavesPerBlock = kBlockThreads / 64;
+constexpr int kControlThreads = 64;
 constexpr int kRaysPerLane = 1536 / 64;    // 24
 constexpr unsigned kMaxBlocks = 1u << 20;
 constexpr unsigned kScanBlocks = 256 * 4;   // persistent scan grid: 4 per CU
@@ -748,8 +749,47 @@ struct OnboardRows {
     float *tactical;
     float *prior;
     float *diag;
+    float *proprio;      // optional [batch, 91]: tactical -> 52..75, prior -> 76..90
+    float *mission_vec;  // optional [batch, 49]: tactical -> 10..33, prior -> 34..48
     size_t batch;
 };
+
+// log1p(x) for x >= 0 (any magnitude): 1 + x = u + c exactly (Fast2Sum),
+// log1p(x) = log2(u)*ln2 + c/u with ln2 as a hi+lo pair.
+__device__ __forceinline__ float log1p_pos(float x) {
+    const float a = fmaxf(x, 1.0f), b = fminf(x, 1.0f);
+    const float u = a + b;
+    const float c = b - (u - a);
+    const float l2 = __builtin_amdgcn_logf(u);
+    const float t = c * __builtin_amdgcn_rcpf(u);
+    const float r = __builtin_fmaf(l2, 0x1.62e43p-1f, __builtin_fmaf(l2, -0x1.05c61p-29f, t));
+    return x == 0.0f ? x : r;
+}
+
+__device__ __forceinline__ float actor_scale(int i) {  // network_gpu.cu:287-293
+    if (i < 3) return 0.05f;
+    if (i < 6) return 0.10f;
+    if (i >= 10 && i < 13) return 0.20f;
+    if (i >= 13 && i < 16) return 0.10f;
+    if (i >= 28 && i < 32) return 0.50f;
+    if (i >= 32 && i < 36) return 0.20f;
+    return 1.0f;
+}
+
+// network_gpu.cu:285-297 (scalar_inputs): lanes 0..51 of a wave write the
+// environment's 52 symlog scalars, lanes 52..61 its 10 finite mission values.
+__device__ __forceinline__ void actor_scalars(const float *obs, const float *mission, int lane,
+                                              float *proprio, float *mission_vec) {
+    if (lane < 52) {
+        float raw = lane < 48 ? obs[lane] : obs[4144 + lane - 48];
+        raw = __builtin_isfinite(raw) ? fmaxf(-1000.0f, fminf(1000.0f, raw)) : 0.0f;
+        const float symlog = copysignf(log1p_pos(fabsf(raw * actor_scale(lane))), raw);
+        proprio[lane] = fmaxf(-8.0f, fminf(8.0f, symlog / sqrtf(1.0001f)));
+    } else if (lane < 62) {
+        const float m = mission[lane - 52];
+        mission_vec[lane - 52] = __builtin_isfinite(m) ? m : 0.0f;
+    }
+}
 
 // Phase 1: one wave per environment scans the LiDAR (persistent blocks share
 // one LDS copy of the ray table).  The 32-byte result is
@@ -780,14 +820,22 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
             park[5] = __int_as_float(s.min_ray);
             park[6] = __int_as_float(s.cluster_count);
         }
+        if (rows.proprio)
+            actor_scalars(obs,
+                          reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride),
+                          lane, rows.proprio + env * 91, rows.mission_vec + env * 49);
     }
 }
 
 // Phase 2: one thread per environment runs the tactical features and the
-// controller from the parked scan result.
-__global__ __launch_bounds__(kBlockThreads) void onboard_control_kernel(OnboardRows rows) {
-    for (size_t env = (size_t)blockIdx.x * kBlockThreads + threadIdx.x; env < rows.batch;
-         env += (size_t)gridDim.x * kBlockThreads) {
+// controller from the parked scan result.  The values are formed in
+// registers and then stored to each destination (the tactical / prior rows
+// and, for the actor, their copies in proprio and mission_vec).  The
+// controller needs ~250 VGPRs, so one wave fills a SIMD: 64-thread blocks
+// spread the 256 waves of a 16,384 batch over every CU instead of a quarter.
+__global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(OnboardRows rows) {
+    for (size_t env = (size_t)blockIdx.x * kControlThreads + threadIdx.x; env < rows.batch;
+         env += (size_t)gridDim.x * kControlThreads) {
         const float *obs = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
         const float *mission =
             reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride);
@@ -800,8 +848,27 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_control_kernel(OnboardR
         s.cluster_y_sum = prior[4];
         s.min_ray = __float_as_int(prior[5]);
         s.cluster_count = __float_as_int(prior[6]);
-        tactical_features(obs, mission, rows.tactical + env * 24);
-        prior_features(obs, mission, s, prior);
+        float t[24], n[15];
+        tactical_features(obs, mission, t);
+        prior_features(obs, mission, s, n);
+        float *tac = rows.tactical + env * 24;
+#pragma unroll
+        for (int i = 0; i < 24; ++i) tac[i] = t[i];
+#pragma unroll
+        for (int i = 0; i < 15; ++i) prior[i] = n[i];
+        if (rows.proprio) {
+            float *p = rows.proprio + env * 91, *mv = rows.mission_vec + env * 49;
+#pragma unroll
+            for (int i = 0; i < 24; ++i) {
+                p[52 + i] = t[i];
+                mv[10 + i] = t[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 15; ++i) {
+                p[76 + i] = n[i];
+                mv[34 + i] = n[i];
+            }
+        }
         if (rows.diag) {
             float *d = rows.diag + env * 4;
             d[0] = s.min_r;
@@ -810,6 +877,16 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_control_kernel(OnboardR
             d[3] = (float)s.cluster_count;
         }
     }
+}
+
+int launch_onboard(const OnboardRows &rows, hipStream_t s) {
+    const size_t scan_want = (rows.batch + kWavesPerBlock - 1) / kWavesPerBlock;
+    const unsigned scan_blocks = scan_want > kScanBlocks ? kScanBlocks : (unsigned)scan_want;
+    const size_t ctrl_want = (rows.batch + kControlThreads - 1) / kControlThreads;
+    onboard_scan_kernel<<<scan_blocks, kBlockThreads, 0, s>>>(rows);
+    onboard_control_kernel<<<ctrl_want > kMaxBlocks ? kMaxBlocks : (unsigned)ctrl_want,
+                             kControlThreads, 0, s>>>(rows);
+    return hipGetLastError() == hipSuccess;
 }
 
 }  // namespace
@@ -827,14 +904,135 @@ extern "C" int tb_hip_onboard_tactical_prior_device(const float *obs, const floa
     rows.tactical = tactical;
     rows.prior = prior;
     rows.diag = diag;
+    rows.proprio = nullptr;
+    rows.mission_vec = nullptr;
     rows.batch = batch_size;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const size_t scan_want = (batch_size + kWavesPerBlock - 1) / kWavesPerBlock;
-    const unsigned scan_blocks = scan_want > kScanBlocks ? kScanBlocks : (unsigned)scan_want;
-    const size_t ctrl_want = (batch_size + kBlockThreads - 1) / kBlockThreads;
     (void)hipGetLastError();
-    onboard_scan_kernel<<<scan_blocks, kBlockThreads, 0, s>>>(rows);
-    onboard_control_kernel<<<ctrl_want > kMaxBlocks ? kMaxBlocks : (unsigned)ctrl_want,
-                             kBlockThreads, 0, s>>>(rows);
-    return hipGetLastError() == hipSuccess;
+    return launch_onboard(rows, reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// The 618M actor's sensor preparation, fused (reference
+// src/network/network_gpu.cu:274-304 scalar_inputs, :467-479 lidar_channels,
+// :480-483 camera_luma, launched back to back at :1446-1451).  One workgroup
+// per environment streams the LiDAR block once into the six channel planes
+// and the cameras once into luma, with 16-byte coalesced loads and stores.
+// The onboard scan waves add the 52 symlog scalars and the mission values
+// (lanes idle during the scan's set-up), the control kernel tactical / prior
+// and their copies.  Fusing the scan into the streaming launch was measured
+// slower: next to saturated HBM traffic the scan's dependent loads stall.  Luma is
+// one fused multiply-add, which is what nvcc's default --fmad=true makes of
+// the reference's `(float)b * (1.0f / 255.0f) - 0.5f`.
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+struct ActorRows {
+    const float *obs;
+    const unsigned char *cameras;
+    float *lidar, *luma;
+    size_t batch;
+};
+
+__device__ __forceinline__ f32x4 lidar_channel4(f32x4 r, int kind) {
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float range = r[e];
+        const bool valid = range > 0.0f && __builtin_isfinite(range);
+        const float clamped = fmaxf(0.05f, fminf(30.0f, range));
+        o[e] = kind == 0 ? (valid ? 1.0f / fmaxf(0.2f, clamped) : 0.0f)
+                         : (kind == 1 ? (valid ? clamped / 30.0f : 1.0f) : (valid ? 1.0f : 0.0f));
+    }
+    return o;
+}
+
+__global__ __launch_bounds__(256) void actor_stream_kernel(ActorRows rows) {
+    const int t = threadIdx.x;
+    for (size_t env = blockIdx.x; env < rows.batch; env += gridDim.x) {
+        const f32x4 *lidar = reinterpret_cast<const f32x4 *>(rows.obs + env * 4148 + 48);
+        f32x4 v[4];
+        if (rows.lidar) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = __builtin_nontemporal_load(lidar + t + 256 * k);
+        }
+        u32x4 px[4];
+        if (rows.luma) {
+            const u32x4 *cam = reinterpret_cast<const u32x4 *>(rows.cameras + env * 16384);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) px[k] = __builtin_nontemporal_load(cam + t + 256 * k);
+        }
+        if (rows.lidar) {
+            // float4 j = t + 256k of the block is bins 4(j%512).. of head j/512;
+            // head h feeds channels h, h+2, h+4.
+            f32x4 *dst = reinterpret_cast<f32x4 *>(rows.lidar + env * 12288);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = t + 256 * k, head = j >> 9, q = j & 511;
+#pragma unroll
+                for (int kind = 0; kind < 3; ++kind)
+                    dst[(head + 2 * kind) * 512 + q] = lidar_channel4(v[k], kind);
+            }
+        }
+        if (rows.luma) {
+            f32x4 *dst = reinterpret_cast<f32x4 *>(rows.luma + env * 16384);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int j = t + 256 * k;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const unsigned w = px[k][d];
+                    f32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        o[e] = __builtin_fmaf((float)((w >> (8 * e)) & 0xffu), 1.0f / 255.0f,
+                                              -0.5f);
+                    dst[4 * j + d] = o;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" int tb_hip_actor_inputs_device(const float *obs, const float *mission,
+                                          const unsigned char *cameras, float *proprio,
+                                          float *mission_vec, float *tactical, float *prior,
+                                          float *lidar_channels, float *camera_luma,
+                                          size_t batch_size, void *stream) {
+    if (!obs || !mission || !proprio || !mission_vec || !tactical || !prior || batch_size == 0 ||
+        batch_size > kMaxBatch || (camera_luma && !cameras))
+        return 0;
+    const uintptr_t align = reinterpret_cast<uintptr_t>(obs) |
+                            reinterpret_cast<uintptr_t>(lidar_channels) |
+                            reinterpret_cast<uintptr_t>(camera_luma) |
+                            reinterpret_cast<uintptr_t>(cameras);
+    if ((align & 15u) != 0) return 0;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    (void)hipGetLastError();
+    if (lidar_channels || camera_luma) {
+        ActorRows ar;
+        ar.obs = obs;
+        ar.cameras = cameras;
+        ar.lidar = lidar_channels;
+        ar.luma = camera_luma;
+        ar.batch = batch_size;
+        actor_stream_kernel<<<batch_size > kMaxBlocks ? kMaxBlocks : (unsigned)batch_size, 256, 0,
+                              s>>>(ar);
+    }
+    OnboardRows rows;
+    rows.obs = reinterpret_cast<const unsigned char *>(obs);
+    rows.obs_stride = 4148 * sizeof(float);
+    rows.mission = reinterpret_cast<const unsigned char *>(mission);
+    rows.mission_stride = 10 * sizeof(float);
+    rows.tactical = tactical;
+    rows.prior = prior;
+    rows.diag = nullptr;
+    rows.proprio = proprio;
+    rows.mission_vec = mission_vec;
+    rows.batch = batch_size;
+    return launch_onboard(rows, s);
 }

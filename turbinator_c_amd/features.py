@@ -84,6 +84,15 @@ def onboard_tactical_prior_device(obs, mission, tactical, prior, diag, batch_siz
         _stream(stream))
 
 
+def actor_inputs_device(obs, mission, cameras, proprio, mission_vec, tactical, prior,
+                        lidar_channels, camera_luma, batch_size: int, stream=None) -> int:
+    """tb_hip_actor_inputs_device (hip_features.h)."""
+    return hip_lib().tb_hip_actor_inputs_device(
+        _dev(obs), _dev(mission), _dev(cameras), _dev(proprio), _dev(mission_vec),
+        _dev(tactical), _dev(prior), _dev(lidar_channels), _dev(camera_luma), batch_size,
+        _stream(stream))
+
+
 def synchronize(stream=None) -> int:
     """tb_cuda_synchronize (cuda_features.h:20)."""
     return hip_lib().tb_cuda_synchronize(_stream(stream))
@@ -137,4 +146,4 @@ def feature_batch_error(handle) -> str:
 
 __all__ = ["extract_features_device", "extract_features_strided_device",
            "extract_features_diagnostics_device", "extract_features_indexed_device", "extract_features_depth_device",
-           "lidar_transform_device", "onboard_tactical_prior_device", "synchronize", "FeatureBatch", "feature_batch_error"]
+           "lidar_transform_device", "onboard_tactical_prior_device", "actor_inputs_device", "synchronize", "FeatureBatch", "feature_batch_error"]

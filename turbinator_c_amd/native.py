@@ -45,6 +45,7 @@ HIP_SIGNATURES = {
     "tb_hip_extract_features_depth_device":
         (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "tb_hip_lidar_transform_device": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
+    "tb_hip_actor_inputs_device": (c_int, [c_void_p] * 9 + [c_size_t, c_void_p]),
     "tb_hip_onboard_tactical_prior_device":
         (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
 }
