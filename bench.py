@@ -226,6 +226,40 @@ def suite(torch, sets, threads: int, steps: int) -> list:
                        note="bytes_per_env: inputs once + every output once"))
     del a_pro, a_mis, a_lid, a_lum
 
+    # f4: the compact SAC actor (hidden 128, the reference default) acting on
+    # the device-resident features of the headline batch.
+    from turbinator_c_amd import actor
+    hidden = 128
+    wrng = np.random.default_rng(3)
+    ws = []
+    for (o, i_), nb in actor.layer_shapes(hidden):
+        ws.append(torch.from_numpy((wrng.standard_normal((o, i_)) * np.sqrt(2.0 / (o + i_)))
+                                   .astype(np.float32)).cuda())
+        ws.append(torch.zeros(nb, dtype=torch.float32, device="cuda"))
+    packed = torch.empty(actor.packed_bytes(hidden) // 4, dtype=torch.float32, device="cuda")
+    assert actor.pack_device(*ws, hidden, packed, torch.cuda.current_stream()) == 1
+    normals = torch.randn((BATCH, 15), dtype=torch.float32, device="cuda")
+    acts = torch.empty((BATCH, 15), dtype=torch.float32, device="cuda")
+    logp = torch.empty((BATCH,), dtype=torch.float32, device="cuda")
+    flops_env = 2 * (142 * hidden + hidden * hidden + hidden * 30)
+
+    def actor_only(i, s):
+        feats = sets[i % len(sets)][3]
+        assert actor.act_device(packed, hidden, feats, normals, acts, logp, None, BATCH, s) == 1
+    per = _events_time(torch, actor_only, steps, 5)
+    tf = flops_env * BATCH / per / 1e12
+    out.append(_report("compact SAC actor, hidden 128, stochastic (16,384 feature rows)",
+                       per, BATCH, None, flops_per_env=flops_env, achieved_TFLOPs=round(tf, 2),
+                       frac_of_fp32_mfma_peak=round(tf / 157.3, 4)))
+
+    def features_then_actor(i, s):
+        o, m, c, f = sets[i % len(sets)]
+        assert features.extract_features_device(o, m, c, f, BATCH, s) == 1
+        assert actor.act_device(packed, hidden, f, normals, acts, logp, None, BATCH, s) == 1
+    out.append(_report("sensor features + compact actor, on device (16,384 envs)",
+                       _events_time(torch, features_then_actor, steps, 5), BATCH, None))
+    del packed, normals, acts, logp, ws
+
     # Configuration 5: 65,536 replay records of 66,672 B, features in place.
     n5, rec = 65536, 66672
     buf = np.zeros(n5 * rec, np.uint8)

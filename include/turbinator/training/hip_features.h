@@ -10,6 +10,7 @@
 #define TURBINATOR_HIP_FEATURES_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -129,6 +130,49 @@ int tb_hip_actor_inputs_device(const float *obs, const float *mission,
                                float *mission_vec, float *tactical, float *prior,
                                float *lidar_channels, float *camera_luma,
                                size_t batch_size, void *stream);
+
+/* Batched compact SAC actor: tb_sac_act_features (src/training/training.c:
+ * 382-392 -> tb_actor_sample :306-329 -> tb_net_forward :219-233) for a whole
+ * batch of device-resident feature rows, so features need not return to the
+ * host between extraction and acting.
+ *
+ * Weights come in the reference's tb_dense layout, one network of
+ * 142 -> hidden -> hidden -> 30 (hidden 16..256): w0[hidden][142], b0[hidden],
+ * w1[hidden][hidden], b1[hidden], w2[30][hidden], b2[30].  They are packed
+ * once per weight update into a device buffer of
+ * tb_hip_sac_actor_packed_bytes(hidden) bytes (16-byte aligned), which the
+ * act entry reads; packed_bytes returns 0 for a hidden width out of range. */
+size_t tb_hip_sac_actor_packed_bytes(int hidden);
+int tb_hip_sac_actor_pack_device(const float *w0, const float *b0, const float *w1,
+                                 const float *b1, const float *w2, const float *b2,
+                                 int hidden, void *packed, void *stream);
+
+/* features [batch,142] -> actions [batch,15] in [-1,1].  normals [batch,15]
+ * are the standard normal draws of the stochastic policy (the reference
+ * scales draw 14 by 0.15 itself); NULL selects the deterministic action, as
+ * deterministic = 1 does.  log_prob [batch] (nullable) receives the
+ * tanh-squashed Gaussian log-probability, 0 when deterministic.  raw
+ * [batch,30] (nullable) receives the network outputs before sampling (15
+ * means, 15 unclamped log-std).  Returns 0 for NULL packed / features /
+ * actions, a hidden width out of range, misaligned packed weights, batch 0
+ * or above 0x7fffffff. */
+int tb_hip_sac_actor_act_device(const void *packed, int hidden, const float *features,
+                                const float *normals, float *actions, float *log_prob,
+                                float *raw, size_t batch_size, void *stream);
+
+/* Host side.  Reads the actor of a tb_sac_save checkpoint (training.c:
+ * 580-590, 605-620) as the concatenation w0 b0 w1 b1 w2 b2 above.  Returns
+ * the number of floats the actor has (weights are written only when
+ * `weights` holds that many; pass NULL to query), with the hidden width and
+ * the agent's rng state in the optional out-parameters; 0 for a missing or
+ * malformed file. */
+size_t tb_hip_sac_read_actor(const char *path, float *weights, size_t capacity, int *hidden,
+                             uint64_t *rng_state);
+
+/* The agent's normal stream (training.c:82-100) from `*state`, which is
+ * advanced: 15 draws per environment in order reproduce what consecutive
+ * stochastic tb_sac_act_features calls consume. */
+void tb_hip_sac_normals(uint64_t *state, float *out, size_t count);
 
 #ifdef __cplusplus
 }

@@ -48,6 +48,10 @@ def lib() -> ctypes.CDLL:
         l.orc_onboard_env.restype = None
         l.orc_actor_inputs_env.argtypes = [c_void_p] * 9
         l.orc_actor_inputs_env.restype = None
+        l.orc_sac_normals.argtypes = [c_void_p, c_void_p, c_size_t]
+        l.orc_sac_normals.restype = None
+        l.orc_sac_actor_env.argtypes = [c_void_p] * 6 + [c_int] + [c_void_p] * 5
+        l.orc_sac_actor_env.restype = None
         l.orc_onboard_ray_dir.argtypes = [c_int, c_void_p]
         l.orc_onboard_ray_dir.restype = None
         _orc = l
@@ -61,6 +65,16 @@ def ref_lib() -> ctypes.CDLL | None:
         l = ctypes.CDLL(str(LIB_REF))
         l.tb_train_extract_features_cpu.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p]
         l.tb_train_extract_features_cpu.restype = None
+        l.tb_train_config_default.argtypes = [c_void_p]
+        l.tb_train_config_default.restype = None
+        l.tb_sac_create.argtypes = [c_void_p]
+        l.tb_sac_create.restype = c_void_p
+        l.tb_sac_destroy.argtypes = [c_void_p]
+        l.tb_sac_destroy.restype = None
+        l.tb_sac_save.argtypes = [c_void_p, ctypes.c_char_p]
+        l.tb_sac_save.restype = c_int
+        l.tb_sac_act_features.argtypes = [c_void_p, c_void_p, c_int, c_void_p, c_void_p]
+        l.tb_sac_act_features.restype = c_int
         _ref = l
     return _ref
 
@@ -170,3 +184,40 @@ def diagnostics(obs: np.ndarray, cameras: np.ndarray | None) -> np.ndarray:
         lib().orc_diagnostics_env(np.ascontiguousarray(obs[e], np.float32).ctypes.data, cam,
                                   out[e].ctypes.data)
     return out
+
+
+class SacActorWeights:
+    """Actor weights in the reference's tb_dense layout (training.c:13-16)."""
+
+    def __init__(self, w0, b0, w1, b1, w2, b2):
+        self.w0, self.b0, self.w1, self.b1, self.w2, self.b2 = (
+            np.ascontiguousarray(a, np.float32) for a in (w0, b0, w1, b1, w2, b2))
+        self.hidden = self.b0.shape[0]
+
+    def arrays(self):
+        return self.w0, self.b0, self.w1, self.b1, self.w2, self.b2
+
+
+def sac_normals(state: int, count: int) -> tuple[np.ndarray, int]:
+    """`count` draws of the agent's tb_normal stream from rng state `state`;
+    returns (draws, state afterwards)."""
+    st = np.array([state], np.uint64)
+    out = np.empty(count, np.float32)
+    lib().orc_sac_normals(st.ctypes.data, _p(out), count)
+    return out, int(st[0])
+
+
+def sac_actor(weights: SacActorWeights, features: np.ndarray, normals: np.ndarray | None):
+    """(action [B,15], log_prob [B], raw [B,30]) of the compact actor per row."""
+    f = np.ascontiguousarray(features, np.float32)
+    b = f.shape[0]
+    act = np.empty((b, 15), np.float32)
+    lp = np.empty(b, np.float32)
+    raw = np.empty((b, 30), np.float32)
+    nrm = None if normals is None else np.ascontiguousarray(normals, np.float32).reshape(b, 15)
+    w = weights.arrays()
+    for e in range(b):
+        lib().orc_sac_actor_env(*(a.ctypes.data for a in w), weights.hidden, f[e].ctypes.data,
+                                None if nrm is None else nrm[e].ctypes.data,
+                                act[e].ctypes.data, lp[e:].ctypes.data, raw[e].ctypes.data)
+    return act, lp, raw

@@ -65,6 +65,14 @@ void orc_actor_inputs_env(const float *obs, const float *mission, const uint8_t 
                           float *proprio, float *mission_vec, float *tactical, float *prior,
                           float *lidar, float *luma);
 
+/* Compact SAC actor (training.c:82-100, 219-233, 306-329): the agent's
+ * normal draws, and one environment's action / log-probability / raw
+ * network outputs (raw_out may be NULL; normals NULL = deterministic). */
+void orc_sac_normals(uint64_t *state, float *out, size_t count);
+void orc_sac_actor_env(const float *w0, const float *b0, const float *w1, const float *b1,
+                       const float *w2, const float *b2, int hidden, const float *feature,
+                       const float *normals, float *action, float *log_prob, float *raw_out);
+
 /* Body-frame direction of onboard ray head*768 + el*128 + azi. */
 void orc_onboard_ray_dir(int ray, float *xyz);
 

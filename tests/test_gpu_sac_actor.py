@@ -1,0 +1,189 @@
+"""GPU parity of the batched compact SAC actor (tb_hip_sac_actor_pack_device
++ tb_hip_sac_actor_act_device) against the CPU oracle, which reproduces
+tb_sac_act_features bit for bit (tests/test_sac_actor_oracle.py).
+
+The matrix cores sum in another order than the reference's sequential loop,
+and tanhf / expf / logf are the device library's, so each output is held to
+a bound set by its own conditioning:
+  * raw outputs: 1e-5 (1 + S), S = |b2| + sum_k |w2_k h1_k| the magnitude of
+    the final layer's summands (float64, from the weights);
+  * actions: (1 - a^2) dz + 2.4e-7, dz the raw bound of the mean plus the
+    exp-rounding of std * eps (tanh' = 1 - a^2; 2.4e-7 = tanh rounding);
+  * log-probability: 1e-4 (1 + |lp|) plus, per action, the log-std bound and
+    the reference formula's sensitivity to the action, 2|a| / (1 - a^2 + 1e-6),
+    times the action bound.  Near |a| = 1 log(1 - a^2 + 1e-6) amplifies one
+    ulp of the action by ~1e6, so a flat bound would be loose or wrong;
+  * deterministic calls: log-probability exactly 0, as the reference leaves it.
+"""
+from __future__ import annotations
+
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.test_sac_actor_oracle import random_features, reference_agent
+from turbinator_c_amd import actor
+
+pytestmark = pytest.mark.gpu
+
+
+def note(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def random_weights(hidden: int, seed: int, gain: float = 1.0) -> list[np.ndarray]:
+    rng = np.random.default_rng(seed)
+    out = []
+    for (o, i), b in actor.layer_shapes(hidden):
+        out.append((rng.standard_normal((o, i)) * gain * np.sqrt(2.0 / (o + i))).astype(
+            np.float32))
+        out.append((rng.standard_normal(b) * 0.1 * gain).astype(np.float32))
+    return out
+
+
+def run_gpu(torch, weights, hidden, feats, draws, want_raw=True):
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()   # noqa: E731
+    b = feats.shape[0]
+    nbytes = actor.packed_bytes(hidden)
+    assert nbytes > 0
+    packed = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda")
+    dw = [dev(w) for w in weights]
+    s = torch.cuda.current_stream()
+    assert actor.pack_device(*dw, hidden, packed, s) == 1
+    f = dev(feats)
+    n = None if draws is None else dev(draws)
+    act = torch.full((b, 15), float("nan"), dtype=torch.float32, device="cuda")
+    lp = torch.full((b,), float("nan"), dtype=torch.float32, device="cuda")
+    raw = torch.full((b, 30), float("nan"), dtype=torch.float32, device="cuda") \
+        if want_raw else None
+    assert actor.act_device(packed, hidden, f, n, act, lp, raw, b, s) == 1
+    torch.cuda.synchronize()
+    return act.cpu().numpy(), lp.cpu().numpy(), None if raw is None else raw.cpu().numpy()
+
+
+def summand_scale(weights, feats) -> np.ndarray:
+    """S = |b2| + |h1| @ |w2|^T per (row, output), in float64."""
+    w0, b0, w1, b1, w2, b2 = (np.asarray(x, np.float64) for x in weights)
+    with np.errstate(invalid="ignore", over="ignore"):
+        h1 = np.tanh(np.tanh(feats.astype(np.float64) @ w0.T + b0) @ w1.T + b1)
+        out = np.abs(b2) + np.abs(h1) @ np.abs(w2).T
+    return np.nan_to_num(out, nan=0.0, posinf=0.0)
+
+
+def check(got, want, weights, feats, draws, label):
+    (ga, glp, graw), (wa, wlp, wraw) = got, want
+    scale = np.ones(15)
+    scale[14] = 0.15
+    eps = np.zeros(wa.shape) if draws is None else np.abs(draws * scale)
+    raw_tol = 1e-5 * (1 + summand_scale(weights, feats))
+    if graw is not None:
+        finite = np.isfinite(wraw)
+        assert np.array_equal(finite, np.isfinite(graw)), f"{label}: raw finiteness"
+        bad = finite & (np.abs(np.where(finite, graw - wraw, 0)) > raw_tol)
+        assert not bad.any(), f"{label}: raw {np.argwhere(bad)[:3]}"
+    a = wa.astype(np.float64)
+    std = np.exp(np.clip(np.nan_to_num(wraw[:, 15:].astype(np.float64)), -3.5, -1.6))
+    # mean error + std * eps error (expf rounding and the log-std error)
+    dz = raw_tol[:, :15] + std * eps * (1e-6 + raw_tol[:, 15:])
+    tol_a = (1 - a * a) * dz + 2.4e-7
+    da = np.abs(ga - a)
+    assert np.all(da <= tol_a), f"{label}: action {np.argwhere(da > tol_a)[:3]}"
+    if draws is None:
+        assert np.all(glp == 0), label
+        return {"action_max": float(da.max())}
+    sens = 2 * np.abs(a) / (1 - a * a + 1e-6)
+    tol = 1e-4 * (1 + np.abs(wlp)) + (raw_tol[:, 15:] + sens * tol_a).sum(1)
+    dl = np.abs(glp.astype(np.float64) - wlp)
+    assert np.all(dl <= tol), f"{label}: log_prob env {np.argmax(dl - tol)}"
+    return {"action_max": float(da.max()), "logp_max": float(dl.max())}
+
+
+@pytest.mark.parametrize("hidden", [16, 37, 128, 256])
+def test_random_weights(torch_cuda, hip, hidden):
+    note(f"sac actor hidden {hidden}, 1000 envs")
+    w = random_weights(hidden, seed=hidden)
+    feats = random_features(1000, seed=7 * hidden)
+    draws = np.random.default_rng(hidden).standard_normal((1000, 15)).astype(np.float32)
+    ow = oracle.SacActorWeights(*w)
+    for d in (None, draws):
+        got = run_gpu(torch_cuda, w, hidden, feats, d)
+        stats = check(got, oracle.sac_actor(ow, feats, d), w, feats, d, f"h{hidden}")
+        note(f"hidden {hidden} {'det' if d is None else 'stoch'}: {stats}")
+
+
+def test_saturating_and_special_rows(torch_cuda, hip):
+    """Large weights push z past +-8 and log-std past both clamps; NaN / Inf
+    features propagate to the raw outputs, which the sampler maps to 0."""
+    note("sac actor saturation and special rows")
+    hidden = 64
+    w = random_weights(hidden, seed=3, gain=12.0)
+    feats = random_features(256, seed=11)
+    feats[3, 5] = np.nan
+    feats[4, 7] = np.inf
+    feats[5] = 1e30
+    draws = np.random.default_rng(4).standard_normal((256, 15)).astype(np.float32) * 3
+    ow = oracle.SacActorWeights(*w)
+    got = run_gpu(torch_cuda, w, hidden, feats, draws)
+    stats = check(got, oracle.sac_actor(ow, feats, draws), w, feats, draws, "saturating")
+    note(f"saturating: {stats}")
+
+
+@pytest.mark.parametrize("batch", [1, 15, 63, 65, 16384])
+def test_batch_tails(torch_cuda, hip, batch):
+    note(f"sac actor batch {batch}")
+    hidden = 128
+    w = random_weights(hidden, seed=batch)
+    feats = random_features(batch, seed=batch + 1) if batch > 3 else \
+        np.random.default_rng(batch).uniform(-1, 1, (batch, 142)).astype(np.float32)
+    draws = np.random.default_rng(batch).standard_normal((batch, 15)).astype(np.float32)
+    got = run_gpu(torch_cuda, w, hidden, feats, draws)
+    pick = np.arange(batch) if batch <= 1024 else \
+        np.random.default_rng(2).choice(batch, 1024, replace=False)
+    want = oracle.sac_actor(oracle.SacActorWeights(*w), feats[pick], draws[pick])
+    check(tuple(g[pick] for g in got), want, w, feats[pick], draws[pick], f"batch{batch}")
+
+
+def test_reference_checkpoint(torch_cuda, hip, tmp_path):
+    """A checkpoint the reference wrote, its own random stream: the GPU batch
+    equals consecutive tb_sac_act_features calls within the tolerances."""
+    if oracle.ref_lib() is None:
+        pytest.skip("oracle/_ref not built")
+    note("sac actor from a reference checkpoint")
+    ref, agent, path = reference_agent(tmp_path, 128, seed=5)
+    try:
+        weights, hidden, rng = actor.read_checkpoint_actor(str(path))
+        feats = random_features(300, seed=21)
+        draws, _ = actor.normals(rng, 300 * 15)
+        draws = draws.reshape(300, 15)
+        want_a = np.empty((300, 15), np.float32)
+        want_lp = np.empty(300, np.float32)
+        for e in range(300):
+            assert ref.tb_sac_act_features(agent, feats[e].ctypes.data, 0,
+                                           want_a[e].ctypes.data, want_lp[e:].ctypes.data) == 1
+        got = run_gpu(torch_cuda, weights, hidden, feats, draws)
+        want = oracle.sac_actor(oracle.SacActorWeights(*weights), feats, draws)
+        assert np.array_equal(want[0].view(np.uint32), want_a.view(np.uint32))
+        assert np.array_equal(want[1].view(np.uint32), want_lp.view(np.uint32))
+        check(got, want, weights, feats, draws, "checkpoint")
+    finally:
+        ref.tb_sac_destroy(agent)
+
+
+def test_argument_validation(hip):
+    lib = hip.hip_lib()
+    d = ctypes.c_void_p(256)
+    odd = ctypes.c_void_p(264)
+    pack, act = lib.tb_hip_sac_actor_pack_device, lib.tb_hip_sac_actor_act_device
+    assert pack(None, d, d, d, d, d, 128, d, None) == 0
+    assert pack(d, d, d, d, d, d, 15, d, None) == 0
+    assert pack(d, d, d, d, d, d, 128, odd, None) == 0
+    assert act(None, 128, d, None, d, None, None, 1, None) == 0
+    assert act(d, 257, d, None, d, None, None, 1, None) == 0
+    assert act(odd, 128, d, None, d, None, None, 1, None) == 0
+    assert act(d, 128, None, None, d, None, None, 1, None) == 0
+    assert act(d, 128, d, None, None, None, None, 1, None) == 0
+    assert act(d, 128, d, None, d, None, None, 0, None) == 0

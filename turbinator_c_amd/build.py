@@ -37,8 +37,8 @@ HIP_FLAGS = [
 C_FLAGS = ["-O2", "-std=c11", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__",
            f"-I{ROCM / 'include'}", f"-I{INCLUDE}"]
 
-HIP_SOURCES = ["features.hip", "onboard.hip"]
-HOST_C_SOURCES = ["feature_batch.c"]
+HIP_SOURCES = ["features.hip", "onboard.hip", "sac_actor.hip"]
+HOST_C_SOURCES = ["feature_batch.c", "sac_host.c"]
 
 LIB_HIP = PKG / "libturbinator_hip.so"
 LIB_SYNTH = PKG / "libturbinator_synth.so"

@@ -46,6 +46,12 @@ HIP_SIGNATURES = {
         (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "tb_hip_lidar_transform_device": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "tb_hip_actor_inputs_device": (c_int, [c_void_p] * 9 + [c_size_t, c_void_p]),
+    "tb_hip_sac_actor_packed_bytes": (c_size_t, [c_int]),
+    "tb_hip_sac_actor_pack_device": (c_int, [c_void_p] * 6 + [c_int, c_void_p, c_void_p]),
+    "tb_hip_sac_actor_act_device":
+        (c_int, [c_void_p, c_int] + [c_void_p] * 5 + [c_size_t, c_void_p]),
+    "tb_hip_sac_read_actor": (c_size_t, [c_char_p, c_void_p, c_size_t, c_void_p, c_void_p]),
+    "tb_hip_sac_normals": (None, [c_void_p, c_void_p, c_size_t]),
     "tb_hip_onboard_tactical_prior_device":
         (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
 }
