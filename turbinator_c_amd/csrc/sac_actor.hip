@@ -33,6 +33,7 @@ constexpr int kFeatures = 142;
 constexpr int kActions = 15;
 constexpr int kRaw = 2 * kActions;
 constexpr int kFeatureChunks = 9;  // 142 inputs padded to 144
+constexpr int kRounds = 4;         // 16 x 15 (environment, action) slots over 64 lanes
 constexpr int kMinHidden = 16, kMaxHidden = 256;
 constexpr float kPi = 3.14159265358979323846f;
 constexpr size_t kMaxBatch = 0x7fffffffu;
@@ -113,38 +114,68 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, un
                                              kBufferWord3);
 }
 
+// Hidden-layer tanh from tanh(x) = 1 - 2 / (e^{2x} + 1) with the hardware
+// exp2 and reciprocal: absolute error ~2e-7 (the reference's tanhf is within
+// an ulp), infinities give +-1 and NaN stays NaN.  The next layer only sums
+// these values, so an absolute bound is what matters; the action's own tanh
+// uses the device library's tanhf.
+__device__ __forceinline__ float tanh_hidden(float x) {
+    const float e = __builtin_amdgcn_exp2f(x * 2.88539008177792681f);  // 2 / ln 2
+    return __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+}
+
 // One dense layer for the wave's 16 environments: out tile nt = W[tile nt] *
 // in^T + b, fragments as described at the top of the file.  Output tiles are
-// done in groups of up to 8; within a group the weights of input chunk s+1 are
-// loaded while chunk s runs on the matrix cores (one chunk is >= 32 MFMAs of
-// 32 cycles, far longer than an L2 hit), and the scheduling barriers keep the
-// compiler from hoisting every load of the layer into registers at once.
-template <int KC, int NT, bool TANH>
+// done in groups of up to 8.  The weight chunk of the step after the current
+// one is always in flight while the current chunk runs on the matrix cores
+// (>= 32 MFMAs of 32 cycles, longer than an L2 hit): within a group, into the
+// next group, and from a layer's last step into the next layer's first chunk,
+// which is handed over in `first`.  The bias is loaded when a group starts and
+// added when it ends.  The scheduling barriers keep the compiler from hoisting
+// every load of the layer into registers at once.
+constexpr int kGroup = 8;
+
+template <int KC, int NT, bool TANH, int KCN, int NTN>
 __device__ __forceinline__ void dense_layer(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
-                                            unsigned b_off, const f32x4 (&in)[KC],
-                                            f32x4 (&out)[NT], int lane) {
-    constexpr int G = NT < 8 ? NT : 8;
+                                            unsigned b_off, unsigned next_w_off,
+                                            const f32x4 (&in)[KC], f32x4 (&out)[NT],
+                                            f32x4 (&first)[kGroup], int lane) {
+    constexpr int G = NT < kGroup ? NT : kGroup;
     const int g = lane >> 4;
     const unsigned wlane = 16u * lane;
+    f32x4 wc[kGroup], wn[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) wc[i] = first[i];
 #pragma unroll
     for (int g0 = 0; g0 < NT; g0 += G) {
-        f32x4 acc[G], wc[G], wn[G];
+        f32x4 acc[G], bias[G];
 #pragma unroll
         for (int i = 0; i < G; ++i)
             if (g0 + i < NT) {
-                acc[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rsrc, 16u * g, b_off + 64u * (g0 + i), 0);
-                wc[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rsrc, wlane, w_off + 1024u * ((g0 + i) * KC), 0);
+                acc[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+                bias[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16u * g,
+                                                                b_off + 64u * (g0 + i), 0);
             }
 #pragma unroll
         for (int s = 0; s < KC; ++s) {
-            if (s + 1 < KC) {
+            if (s + 1 < KC) {  // next chunk of this group
 #pragma unroll
                 for (int i = 0; i < G; ++i)
                     if (g0 + i < NT)
                         wn[i] = __builtin_amdgcn_raw_buffer_load_b128(
                             rsrc, wlane, w_off + 1024u * ((g0 + i) * KC + s + 1), 0);
+            } else if (g0 + G < NT) {  // first chunk of the next group
+#pragma unroll
+                for (int i = 0; i < G; ++i)
+                    if (g0 + G + i < NT)
+                        wn[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                            rsrc, wlane, w_off + 1024u * ((g0 + G + i) * KC), 0);
+            } else if (NTN > 0) {  // first chunk of the next layer
+#pragma unroll
+                for (int i = 0; i < kGroup; ++i)
+                    if (i < NTN)
+                        wn[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                            rsrc, wlane, next_w_off + 1024u * (i * KCN), 0);
             }
 #pragma unroll
             for (int t = 0; t < 4; ++t)
@@ -155,19 +186,20 @@ __device__ __forceinline__ void dense_layer(__amdgpu_buffer_rsrc_t rsrc, unsigne
                                                                       0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < G; ++i) wc[i] = wn[i];
+            for (int i = 0; i < kGroup; ++i) wc[i] = wn[i];
         }
 #pragma unroll
         for (int i = 0; i < G; ++i)
             if (g0 + i < NT) {
-                if (TANH) {
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) out[g0 + i][v] = tanhf(acc[i][v]);
-                } else {
-                    out[g0 + i] = acc[i];
+                for (int v = 0; v < 4; ++v) {
+                    const float y = acc[i][v] + bias[i][v];
+                    out[g0 + i][v] = TANH ? tanh_hidden(y) : y;
                 }
             }
     }
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) first[i] = wc[i];
 }
 
 __device__ __forceinline__ float finite_or_zero(float x) {  // training.c:61-63
@@ -184,6 +216,14 @@ __global__ __launch_bounds__(256) void sac_actor_kernel(ActArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, j = lane & 15;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.packed, a.packed_bytes);
+    // Layer 0's first weight chunk; each pass through the layers leaves the
+    // next pass's first chunk here (the last layer prefetches layer 0).
+    f32x4 first[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i)
+        if (i < HT)
+            first[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                wrs, 16u * lane, a.w_off[0] + 1024u * (i * kFeatureChunks), 0);
     // The loop bound is uniform over the block, so every wave meets the
     // barriers; waves past the batch end compute on zeros and store nothing.
     for (size_t gbase = (size_t)blockIdx.x * 64; gbase < a.batch;
@@ -210,10 +250,23 @@ __global__ __launch_bounds__(256) void sac_actor_kernel(ActArgs a) {
                                         __builtin_amdgcn_raw_buffer_load_b64(frs, off + 8, 0, 0));
             x[s] = (f32x4){lo[0], lo[1], hi[0], hi[1]};
         }
+        // The group's normals (slot p = 15 e + i of environment base + e),
+        // loaded now and used after the three layers.
+        float drawn[kRounds];
+#pragma unroll
+        for (int round = 0; round < kRounds; ++round) {
+            const int p = lane + 64 * round;
+            drawn[round] = 0.0f;
+            if (a.normals && p < 16 * kActions && base + p / kActions < a.batch)
+                drawn[round] = a.normals[base * kActions + p];
+        }
         f32x4 h0[HT], h1[HT], r[2];
-        dense_layer<kFeatureChunks, HT, true>(wrs, a.w_off[0], a.b_off[0], x, h0, lane);
-        dense_layer<HT, HT, true>(wrs, a.w_off[1], a.b_off[1], h0, h1, lane);
-        dense_layer<HT, 2, false>(wrs, a.w_off[2], a.b_off[2], h1, r, lane);
+        dense_layer<kFeatureChunks, HT, true, HT, HT>(wrs, a.w_off[0], a.b_off[0], a.w_off[1], x,
+                                                      h0, first, lane);
+        dense_layer<HT, HT, true, HT, 2>(wrs, a.w_off[1], a.b_off[1], a.w_off[2], h0, h1, first,
+                                         lane);
+        dense_layer<HT, 2, false, kFeatureChunks, (HT < kGroup ? HT : kGroup)>(
+            wrs, a.w_off[2], a.b_off[2], a.w_off[0], h1, r, first, lane);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
@@ -225,15 +278,16 @@ __global__ __launch_bounds__(256) void sac_actor_kernel(ActArgs a) {
         __syncthreads();
         // training.c:310-327 for the wave's 16 x 15 (environment, action)
         // pairs, consecutive lanes on consecutive action slots.
-        for (int p = lane; p < 16 * kActions; p += 64) {
+#pragma unroll
+        for (int round = 0; round < kRounds; ++round) {
+            const int p = lane + 64 * round;
             const int e = p / kActions, i = p - kActions * e;
             const size_t ge = base + e;
-            if (ge >= a.batch) continue;
+            if (p >= 16 * kActions || ge >= a.batch) continue;
             const float raw_ls = finite_or_zero(raw_s[wave][e][kActions + i]);
             const float log_std = clampf(raw_ls, -3.5f, -1.6f);
             const float sd = expf(log_std);
-            const float eps =
-                a.normals ? a.normals[ge * kActions + i] * (i == 14 ? 0.15f : 1.0f) : 0.0f;
+            const float eps = a.normals ? drawn[round] * (i == 14 ? 0.15f : 1.0f) : 0.0f;
             const float z = clampf(finite_or_zero(raw_s[wave][e][i]) + sd * eps, -8.0f, 8.0f);
             const float act = tanhf(z);
             a.actions[ge * kActions + i] = act;
