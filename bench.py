@@ -307,6 +307,15 @@ def suite(torch, sets, threads: int, steps: int) -> list:
                        note="bytes_per_env counts only the fused minimum"))
     del r_obs, r_mis, r_cam, g_obs, g_mis, g_cam
 
+    out += host_legs(threads)
+    return out
+
+
+def host_legs(threads: int) -> list:
+    """Host-side workloads, PCIe included: the reference's pageable host API
+    and the pinned, double-buffered pipeline."""
+    from turbinator_c_amd import features, synth
+    out = []
     # Host API, PCIe included (pageable copies, as the reference): the
     # trainer's default batch 32 (latency) and the 1,024 cap (bandwidth).
     for n, reps in ((32, 200), (1024, 20)):
@@ -325,6 +334,55 @@ def suite(torch, sets, threads: int, steps: int) -> list:
         out.append(_report(f"host API tb_cuda_extract_features_host, {n} envs (PCIe-inclusive)",
                            per, n, None, note="pageable host memory, synchronous",
                            host_GBs=round(n * (BYTES_PER_ENV - 0) / per / 1e9, 2)))
+
+    # Pinned, double-buffered pipeline (tb_hip_feature_pipeline_*): the
+    # producer's data already sits in the pinned slots; one slot measures
+    # submit + wait latency, two slots the steady state with one batch in
+    # flight while the other is collected and resubmitted.
+    for n, slots, reps in ((32, 1, 200), (32, 2, 200), (1024, 1, 20), (1024, 2, 20),
+                           (16384, 2, 6)):
+        hb = synth.make_batch(n, seed=9, threads=threads)
+        pipe = features.FeaturePipeline.create(0, n, slots)
+        assert pipe is not None, "pipeline create failed"
+        try:
+            for s in range(slots):
+                o, m, c = pipe.inputs(s)
+                o[:] = hb.obs
+                m[:] = hb.mission
+                c[:] = hb.cameras
+            for s in range(slots):
+                assert pipe.submit(s, n) == 1, pipe.error()
+                assert pipe.wait(s, n) is not None, pipe.error()
+            t0 = time.perf_counter()
+            if slots == 1:
+                for _ in range(reps):
+                    assert pipe.submit(0, n) == 1
+                    assert pipe.wait(0, n) is not None
+            else:
+                for s in range(slots):
+                    assert pipe.submit(s, n) == 1
+                for r in range(reps):
+                    s = r % slots
+                    assert pipe.wait(s, n) is not None
+                    assert pipe.submit(s, n) == 1
+                for s in range(slots):
+                    assert pipe.wait(s, n) is not None
+                reps += slots
+            per = (time.perf_counter() - t0) / reps
+            got = pipe.wait(0, n).copy()
+        finally:
+            pipe.destroy()
+        if n <= 1024:
+            import oracle
+            from tests.conftest import assert_feature_parity
+            assert_feature_parity(got, oracle.features(hb.obs, hb.mission, hb.cameras),
+                                  f"pipeline{n}")
+        out.append(_report(f"pinned pipeline, {n} envs, {slots} slot(s) (PCIe-inclusive)",
+                           per, n, None,
+                           note="producer writes the pinned slots in place; "
+                                + ("submit + wait" if slots == 1 else "steady state, "
+                                   "one batch in flight while the other is collected"),
+                           host_GBs=round(n * BYTES_PER_ENV / per / 1e9, 2)))
     return out
 
 
@@ -371,6 +429,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--suite", action="store_true",
                     help="also time the secondary workloads (stderr JSON lines)")
+    ap.add_argument("--host-legs", action="store_true",
+                    help="also time the host API and the pinned pipeline (stderr)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after timing, run 1 GiB device copies (PMC calibration)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -404,6 +464,8 @@ def main() -> int:
         copy_calibration(torch)
     if args.suite:
         suite(torch, sets, threads, args.steps)
+    elif args.host_legs:
+        host_legs(threads)
     bytes_per_call = BYTES_PER_ENV * BATCH
     achieved = bytes_per_call / per_call / 1e9
     traffic = None

@@ -174,6 +174,58 @@ size_t tb_hip_sac_read_actor(const char *path, float *weights, size_t capacity, 
  * stochastic tb_sac_act_features calls consume. */
 void tb_hip_sac_normals(uint64_t *state, float *out, size_t count);
 
+/* Pinned, double-buffered staging for host-side producers: the counterpart
+ * of the reference host object (cuda_features.h:22-34, features.cu:62-88)
+ * for callers that can write their observations into staging memory the
+ * library owns.  A pipeline has `slots` (1..8) slots of `max_batch`
+ * environments each; every slot owns pinned host buffers, device buffers
+ * and a non-blocking stream.  The producer fills a slot's inputs in place
+ * (the arrays returned by _inputs, rows laid out as in the reference ABI:
+ * obs [max_batch,4148] float, mission [max_batch,10] float, cameras
+ * [max_batch,16384] uint8), _submit queues host-to-device copy, extraction
+ * and device-to-host copy of the first `count` rows on the slot's stream and
+ * returns without waiting, and _wait blocks until the slot is done and
+ * returns its pinned [count,142] feature rows (valid until the slot's next
+ * submit).  While a slot is in flight its inputs must not be written.
+ * Not thread-safe per handle; create selects `device_id` on the calling
+ * thread, as the reference create does. */
+enum {
+    TB_HIP_PIPELINE_MAX_SLOTS = 8,
+    TB_HIP_PIPELINE_MAX_BATCH = 0x7fffffff
+};
+
+typedef struct tb_hip_feature_pipeline tb_hip_feature_pipeline;
+
+/* NULL for max_batch 0 or above TB_HIP_PIPELINE_MAX_BATCH, slots outside
+ * 1..8, a device that cannot be selected, or any allocation failure. */
+tb_hip_feature_pipeline *tb_hip_feature_pipeline_create(int device_id, size_t max_batch,
+                                                        int slots);
+
+/* NULL-safe; drains every slot's stream before freeing. */
+void tb_hip_feature_pipeline_destroy(tb_hip_feature_pipeline *pipeline);
+
+/* Last error text ("<stage>: <runtime message>", or a slot-state message
+ * such as "submit: slot 1 is in flight"); a fixed message for NULL. */
+const char *tb_hip_feature_pipeline_error(const tb_hip_feature_pipeline *pipeline);
+
+/* Writes the slot's pinned input arrays to the non-NULL out-parameters.
+ * Returns 0 for a NULL pipeline or a slot out of range. */
+int tb_hip_feature_pipeline_inputs(tb_hip_feature_pipeline *pipeline, int slot, float **obs,
+                                   float **mission, unsigned char **cameras);
+
+/* Queues the slot's first `count` environments.  with_cameras = 0 skips the
+ * camera copy and zeroes features 126..141 (the device entry's NULL-cameras
+ * rule).  Returns 1 when queued; 0 with the error text untouched for a NULL
+ * pipeline, a slot out of range or count outside 1..max_batch; 0 with the
+ * error set when the slot is still in flight or a runtime call fails. */
+int tb_hip_feature_pipeline_submit(tb_hip_feature_pipeline *pipeline, int slot, size_t count,
+                                   int with_cameras);
+
+/* Waits for the slot and returns its feature rows, or NULL (error set) when
+ * the slot has never been submitted or the stream failed.  Waiting again on
+ * a completed slot returns the same rows. */
+const float *tb_hip_feature_pipeline_wait(tb_hip_feature_pipeline *pipeline, int slot);
+
 #ifdef __cplusplus
 }
 #endif

@@ -88,6 +88,17 @@ def test_argument_validation_without_gpu():
     assert lib.tb_cuda_feature_batch_error(None) == b"CUDA feature batch unavailable"
     lib.tb_cuda_feature_batch_destroy(None)
     assert lib.tb_cuda_extract_features_host(None, dummy, dummy, dummy, 1, dummy) == 0
+    # Pipeline: invalid create arguments -> NULL before any device call;
+    # NULL handles are rejected.
+    assert not lib.tb_hip_feature_pipeline_create(0, 0, 2)
+    assert not lib.tb_hip_feature_pipeline_create(0, 0x80000000, 2)
+    assert not lib.tb_hip_feature_pipeline_create(0, 4, 0)
+    assert not lib.tb_hip_feature_pipeline_create(0, 4, 9)
+    assert lib.tb_hip_feature_pipeline_error(None) == b"HIP feature pipeline unavailable"
+    lib.tb_hip_feature_pipeline_destroy(None)
+    assert lib.tb_hip_feature_pipeline_inputs(None, 0, None, None, None) == 0
+    assert lib.tb_hip_feature_pipeline_submit(None, 0, 1, 1) == 0
+    assert not lib.tb_hip_feature_pipeline_wait(None, 0)
 
 
 def test_missing_library_fails_loudly(tmp_path, monkeypatch):

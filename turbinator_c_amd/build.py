@@ -38,7 +38,7 @@ C_FLAGS = ["-O2", "-std=c11", "-fPIC", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD
            f"-I{ROCM / 'include'}", f"-I{INCLUDE}"]
 
 HIP_SOURCES = ["features.hip", "onboard.hip", "sac_actor.hip"]
-HOST_C_SOURCES = ["feature_batch.c", "sac_host.c"]
+HOST_C_SOURCES = ["feature_batch.c", "feature_pipeline.c", "sac_host.c"]
 
 LIB_HIP = PKG / "libturbinator_hip.so"
 LIB_SYNTH = PKG / "libturbinator_synth.so"

@@ -9,6 +9,8 @@ hipStream_t integer or None (null stream).
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 
 from .native import CAMERA_BYTES, FEATURE_DIM, MISSION_DIM, OBS_DIM, hip_lib  # noqa: F401
@@ -144,6 +146,68 @@ def feature_batch_error(handle) -> str:
     return hip_lib().tb_cuda_feature_batch_error(handle).decode()
 
 
+class FeaturePipeline:
+    """tb_hip_feature_pipeline handle (hip_features.h): pinned staging slots
+    the producer writes in place, asynchronous submit, blocking wait."""
+
+    def __init__(self, handle: int, max_batch: int, slots: int):
+        self._handle = handle
+        self.max_batch = max_batch
+        self.slots = slots
+
+    @classmethod
+    def create(cls, device_id: int, max_batch: int, slots: int = 2) -> "FeaturePipeline | None":
+        h = hip_lib().tb_hip_feature_pipeline_create(device_id, max_batch, slots)
+        return cls(h, max_batch, slots) if h else None
+
+    @property
+    def handle(self) -> int | None:
+        return self._handle
+
+    def error(self) -> str:
+        return hip_lib().tb_hip_feature_pipeline_error(self._handle).decode()
+
+    def inputs(self, slot: int):
+        """(obs, mission, cameras) numpy views of the slot's pinned arrays."""
+        o, m, c = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        if hip_lib().tb_hip_feature_pipeline_inputs(self._handle, slot, ctypes.byref(o),
+                                                    ctypes.byref(m), ctypes.byref(c)) != 1:
+            raise ValueError(f"slot {slot} out of range")
+        n = self.max_batch
+
+        def view(addr, ctype, shape):
+            return np.ctypeslib.as_array(ctypes.cast(addr, ctypes.POINTER(ctype)), shape=shape)
+
+        return (view(o.value, ctypes.c_float, (n, OBS_DIM)),
+                view(m.value, ctypes.c_float, (n, MISSION_DIM)),
+                view(c.value, ctypes.c_ubyte, (n, CAMERA_BYTES)))
+
+    def submit(self, slot: int, count: int, with_cameras: bool = True) -> int:
+        return hip_lib().tb_hip_feature_pipeline_submit(self._handle, slot, count,
+                                                        1 if with_cameras else 0)
+
+    def wait(self, slot: int, count: int) -> np.ndarray | None:
+        """The slot's [count,142] pinned feature rows (a view), or None."""
+        addr = hip_lib().tb_hip_feature_pipeline_wait(self._handle, slot)
+        if not addr:
+            return None
+        return np.ctypeslib.as_array(ctypes.cast(addr, ctypes.POINTER(ctypes.c_float)),
+                                     shape=(count, FEATURE_DIM))
+
+    def destroy(self) -> None:
+        if self._handle:
+            hip_lib().tb_hip_feature_pipeline_destroy(self._handle)
+            self._handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.destroy()
+
+
 __all__ = ["extract_features_device", "extract_features_strided_device",
-           "extract_features_diagnostics_device", "extract_features_indexed_device", "extract_features_depth_device",
-           "lidar_transform_device", "onboard_tactical_prior_device", "actor_inputs_device", "synchronize", "FeatureBatch", "feature_batch_error"]
+           "extract_features_diagnostics_device", "extract_features_indexed_device",
+           "extract_features_depth_device", "lidar_transform_device",
+           "onboard_tactical_prior_device", "actor_inputs_device", "synchronize", "FeatureBatch",
+           "feature_batch_error", "FeaturePipeline"]

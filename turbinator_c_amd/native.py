@@ -54,6 +54,12 @@ HIP_SIGNATURES = {
     "tb_hip_sac_normals": (None, [c_void_p, c_void_p, c_size_t]),
     "tb_hip_onboard_tactical_prior_device":
         (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "tb_hip_feature_pipeline_create": (c_void_p, [c_int, c_size_t, c_int]),
+    "tb_hip_feature_pipeline_destroy": (None, [c_void_p]),
+    "tb_hip_feature_pipeline_error": (c_char_p, [c_void_p]),
+    "tb_hip_feature_pipeline_inputs": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
+    "tb_hip_feature_pipeline_submit": (c_int, [c_void_p, c_int, c_size_t, c_int]),
+    "tb_hip_feature_pipeline_wait": (c_void_p, [c_void_p, c_int]),
 }
 
 SYNTH_SIGNATURES = {
