@@ -170,10 +170,45 @@ def _report(name: str, per_call: float, envs: int, bytes_per_env: int | None, **
     return r
 
 
-def suite(torch, sets, threads: int, steps: int) -> list:
-    """Secondary workloads, printed to stderr (the stdout line is the headline)."""
-    from turbinator_c_amd import features, synth
+SUITE_LEGS = ("depth", "diag", "onboard", "actor_prep", "sac_actor", "c5", "replay", "host")
+
+
+def suite(torch, sets, threads: int, steps: int, legs=SUITE_LEGS) -> list:
+    """Secondary workloads, printed to stderr (the stdout line is the headline).
+    `legs` selects a subset of SUITE_LEGS."""
     out = []
+    for leg in SUITE_LEGS:
+        if leg not in legs:
+            continue
+        out += _suite_leg(leg, torch, sets, threads, steps)
+    return out
+
+
+def _suite_leg(leg: str, torch, sets, threads: int, steps: int) -> list:
+    out = []
+    if leg == "host":
+        return host_legs(threads)
+    tac = torch.empty((BATCH, 24), dtype=torch.float32, device="cuda")
+    pri = torch.empty((BATCH, 15), dtype=torch.float32, device="cuda")
+    if leg == "depth":
+        _leg_depth(torch, sets, threads, steps, out)
+    elif leg == "diag":
+        _leg_diag(torch, sets, steps, out)
+    elif leg == "onboard":
+        _leg_onboard(torch, sets, steps, out, tac, pri)
+    elif leg == "actor_prep":
+        _leg_actor_prep(torch, sets, steps, out, tac, pri)
+    elif leg == "sac_actor":
+        _leg_sac_actor(torch, sets, steps, out)
+    elif leg == "c5":
+        _leg_c5(torch, threads, steps, out)
+    elif leg == "replay":
+        _leg_replay(torch, threads, steps, out)
+    return out
+
+
+def _leg_depth(torch, sets, threads, steps, out):
+    from turbinator_c_amd import features, synth
     # fp32 depth cameras: the configurations' literal 4x64x64 fp32 cameras.
     dsets = []
     for k in range(3):
@@ -191,6 +226,9 @@ def suite(torch, sets, threads: int, steps: int) -> list:
                        OBS_B + MISSION_B + 4 * CAMERA_B + OUT_B))
     del dsets
 
+
+def _leg_diag(torch, sets, steps, out):
+    from turbinator_c_amd import features
     diag = torch.empty((BATCH, 224), dtype=torch.int32, device="cuda")
 
     def diag_call(i, s):
@@ -199,8 +237,9 @@ def suite(torch, sets, threads: int, steps: int) -> list:
     out.append(_report("config 3 + diagnostics (224 words/env)",
                        _events_time(torch, diag_call, steps, 5), BATCH, BYTES_PER_ENV + 896))
 
-    tac = torch.empty((BATCH, 24), dtype=torch.float32, device="cuda")
-    pri = torch.empty((BATCH, 15), dtype=torch.float32, device="cuda")
+
+def _leg_onboard(torch, sets, steps, out, tac, pri):
+    from turbinator_c_amd import features
 
     def onboard_call(i, s):
         o, m, _, _ = sets[i % len(sets)]
@@ -208,6 +247,9 @@ def suite(torch, sets, threads: int, steps: int) -> list:
     out.append(_report("onboard tactical+prior (16,384 envs)",
                        _events_time(torch, onboard_call, steps, 5), BATCH, None))
 
+
+def _leg_actor_prep(torch, sets, steps, out, tac, pri):
+    from turbinator_c_amd import features
     # f3: the 618M actor's sensor preparation (network_gpu.cu:1446-1451) fused:
     # proprio 91 + mission 49 + tactical 24 + prior 15 + 6x16x128 LiDAR
     # channels + 4x64x64 luma per environment.
@@ -226,6 +268,9 @@ def suite(torch, sets, threads: int, steps: int) -> list:
                        note="bytes_per_env: inputs once + every output once"))
     del a_pro, a_mis, a_lid, a_lum
 
+
+def _leg_sac_actor(torch, sets, steps, out):
+    from turbinator_c_amd import features
     # f4: the compact SAC actor (hidden 128, the reference default) acting on
     # the device-resident features of the headline batch.
     from turbinator_c_amd import actor
@@ -260,6 +305,9 @@ def suite(torch, sets, threads: int, steps: int) -> list:
                        _events_time(torch, features_then_actor, steps, 5), BATCH, None))
     del packed, normals, acts, logp, ws
 
+
+def _leg_c5(torch, threads, steps, out):
+    from turbinator_c_amd import features, synth
     # Configuration 5: 65,536 replay records of 66,672 B, features in place.
     n5, rec = 65536, 66672
     buf = np.zeros(n5 * rec, np.uint8)
@@ -276,6 +324,9 @@ def suite(torch, sets, threads: int, steps: int) -> list:
                        _events_time(torch, c5_call, max(steps // 4, 10), 3), n5, BYTES_PER_ENV))
     del dbuf, f5
 
+
+def _leg_replay(torch, threads, steps, out):
+    from turbinator_c_amd import features, synth
     # Replay sampling (f1): 16,384 samples from a 65,536-slot SoA replay, fused
     # versus the reference's gather-into-a-batch followed by extraction.
     cap = 65536
@@ -431,6 +482,8 @@ def main() -> int:
                     help="also time the secondary workloads (stderr JSON lines)")
     ap.add_argument("--host-legs", action="store_true",
                     help="also time the host API and the pinned pipeline (stderr)")
+    ap.add_argument("--legs", default=None,
+                    help="comma-separated subset of the --suite workloads: " + ",".join(SUITE_LEGS))
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after timing, run 1 GiB device copies (PMC calibration)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -462,8 +515,13 @@ def main() -> int:
     log(f"[bench] parity sample ok: {stats}")
     if args.copy_calibration:
         copy_calibration(torch)
-    if args.suite:
-        suite(torch, sets, threads, args.steps)
+    if args.suite or args.legs:
+        legs = SUITE_LEGS if not args.legs else tuple(args.legs.split(","))
+        unknown = set(legs) - set(SUITE_LEGS)
+        if unknown:
+            print(f"bench.py: unknown legs {sorted(unknown)}", file=sys.stderr)
+            return 2
+        suite(torch, sets, threads, args.steps, legs)
     elif args.host_legs:
         host_legs(threads)
     bytes_per_call = BYTES_PER_ENV * BATCH

@@ -39,9 +39,9 @@ namespace {
 constexpr int kBlockThreads = 256;
 constexpr int kWavesPerBlock = kBlockThreads / 64;
 constexpr int kControlThreads = 64;
-constexpr int kRaysPerLane = 1536 / 64;    // 24
+constexpr int kScanRays = 1536 / kBlockThreads;  // rays per scan thread
 constexpr unsigned kMaxBlocks = 1u << 20;
-constexpr unsigned kScanBlocks = 256 * 4;   // persistent scan grid: 4 per CU
+constexpr unsigned kScanBlocks = 256 * 8;   // persistent scan grid: 8 per CU
 constexpr size_t kMaxBatch = 0x7fffffffu;
 constexpr float kPi = 3.14159265358979323846f;
 
@@ -109,52 +109,12 @@ __device__ __forceinline__ int dpp_partner(int v) {
     return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
 }
 
-struct LaneKey {      // lexicographic (range, ray) with the winner's offsets
-    float r, dx, dy;
-    int ray;
-};
-
-__device__ __forceinline__ LaneKey key_min(const LaneKey &a, const LaneKey &b) {
-    const bool take_b = b.r < a.r || (b.r == a.r && b.ray < a.ray);
-    return take_b ? b : a;
-}
-
-template <int CTRL>
-__device__ __forceinline__ LaneKey key_partner(const LaneKey &k) {
-    LaneKey p;
-    p.r = __int_as_float(dpp_partner<CTRL>(__float_as_int(k.r)));
-    p.dx = __int_as_float(dpp_partner<CTRL>(__float_as_int(k.dx)));
-    p.dy = __int_as_float(dpp_partner<CTRL>(__float_as_int(k.dy)));
-    p.ray = dpp_partner<CTRL>(k.ray);
-    return p;
-}
-
 template <bool SWAP32>
 __device__ __forceinline__ int swap_pair(int v, int &other) {
     const auto s = SWAP32 ? __builtin_amdgcn_permlane32_swap(v, v, false, false)
                           : __builtin_amdgcn_permlane16_swap(v, v, false, false);
     other = s[1];
     return s[0];
-}
-
-template <bool SWAP32>
-__device__ __forceinline__ LaneKey key_swap_min(const LaneKey &k) {
-    LaneKey a, b;
-    int o;
-    a.r = __int_as_float(swap_pair<SWAP32>(__float_as_int(k.r), o)); b.r = __int_as_float(o);
-    a.dx = __int_as_float(swap_pair<SWAP32>(__float_as_int(k.dx), o)); b.dx = __int_as_float(o);
-    a.dy = __int_as_float(swap_pair<SWAP32>(__float_as_int(k.dy), o)); b.dy = __int_as_float(o);
-    a.ray = swap_pair<SWAP32>(k.ray, o); b.ray = o;
-    return key_min(a, b);
-}
-
-__device__ __forceinline__ LaneKey wave_key_min(LaneKey k) {
-    k = key_min(k, key_partner<0xB1>(k));    // quad_perm [1,0,3,2]
-    k = key_min(k, key_partner<0x4E>(k));    // quad_perm [2,3,0,1]
-    k = key_min(k, key_partner<0x141>(k));   // row_half_mirror
-    k = key_min(k, key_partner<0x140>(k));   // row_mirror
-    k = key_swap_min<false>(k);              // rows 0<->1, 2<->3
-    return key_swap_min<true>(k);            // halves
 }
 
 __device__ __forceinline__ float wave_min(float v) {
@@ -209,70 +169,186 @@ struct RayPlanes {
     float d[3][1536];
 };
 
-// onboard_features.cuh:184-234, one wave per environment.  Pass 1 keeps
-// each ray's corridor centre (x = +inf when the ray is outside the window or
-// the corridor), so pass 2 is a compare-and-accumulate.
-__device__ void scan_lidar(const float *obs, const RayPlanes &rays, int lane, ScanResult &out) {
+// Closest-return key: (range bits << 32) | ray.  Ranges that can win are
+// positive, so unsigned order on the key is the (range, ray) order.
+constexpr uint64_t kNoReturnKey = (uint64_t)0x41f00000u << 32 | 0x7fffffffu;  // (30.0f, none)
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+    const unsigned lo = (unsigned)dpp_partner<CTRL>((int)(unsigned)v);
+    const unsigned hi = (unsigned)dpp_partner<CTRL>((int)(unsigned)(v >> 32));
+    return (uint64_t)hi << 32 | lo;
+}
+
+template <bool SWAP32>
+__device__ __forceinline__ uint64_t swap_min_u64(uint64_t v) {
+    int olo, ohi;
+    const unsigned lo = (unsigned)swap_pair<SWAP32>((int)(unsigned)v, olo);
+    const unsigned hi = (unsigned)swap_pair<SWAP32>((int)(unsigned)(v >> 32), ohi);
+    const uint64_t a = (uint64_t)hi << 32 | lo;
+    const uint64_t b = (uint64_t)(unsigned)ohi << 32 | (unsigned)olo;
+    return b < a ? b : a;
+}
+
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+    uint64_t p = dpp_u64<0xB1>(v);
+    v = p < v ? p : v;
+    p = dpp_u64<0x4E>(v);
+    v = p < v ? p : v;
+    p = dpp_u64<0x141>(v);
+    v = p < v ? p : v;
+    p = dpp_u64<0x140>(v);
+    v = p < v ? p : v;
+    v = swap_min_u64<false>(v);
+    return swap_min_u64<true>(v);
+}
+
+// Per-wave partial results of one environment's scan, exchanged in LDS, and
+// the attitude rows + lateral position of the environment being scanned and
+// of the next one (written by the block's last wave one environment ahead).
+struct ScanShared {
+    uint64_t key[kWavesPerBlock];
+    float min_dx_c[kWavesPerBlock];
+    int count[kWavesPerBlock];
+    double y_sum[kWavesPerBlock];
+    float frame[2][10];  // r[0..8], py
+};
+
+// onboard_features.cuh:105-109,137-145 (attitude) and :183 (py) of one
+// environment, stored for the scan by lane 0 of the calling wave.
+__device__ __forceinline__ void store_frame(const float *obs, float *frame, int lane) {
     const Attitude att =
         attitude_of(ob_obs(obs[6]), ob_obs(obs[7]), ob_obs(obs[8]), ob_obs(obs[9]));
-    const float *r = att.r;
     const float py = ob_obs(obs[1]);
-
-    float range[kRaysPerLane];
+    if (lane == 0) {
 #pragma unroll
-    for (int t = 0; t < kRaysPerLane; ++t) {
-        const int head = t / 12, el = (t % 12) / 2;  // ray = lane + 64t
-        range[t] = ob_obs(__builtin_nontemporal_load(obs + 48 + (head * 16 + el) * 128 +
-                                                      (t & 1) * 64 + lane));
+        for (int k = 0; k < 9; ++k) frame[k] = att.r[k];
+        frame[9] = py;
     }
+}
 
-    LaneKey best = {30.0f, 0.0f, 0.0f, 0x7fffffff};
-    float min_dx_c = 30.0f;
-    float xc[kRaysPerLane], yc[kRaysPerLane];
+// The six ranges thread `tid` of a scan block owns: rays tid + 256u
+// (u = 0..5), i.e. head u / 3, elevation row (tid >> 7) + 2 (u % 3),
+// azimuth tid & 127.  For each u the block reads 256 consecutive floats
+// (two consecutive LiDAR rows).
+__device__ __forceinline__ void load_ranges(const float *obs, int tid, float (&rg)[kScanRays]) {
 #pragma unroll
-    for (int t = 0; t < kRaysPerLane; ++t) {
-        const float rg = range[t];
-        xc[t] = __builtin_huge_valf();
-        yc[t] = 0.0f;
-        if (!(rg > 0.35f && rg < 11.5f)) continue;
-        const int ray = lane + 64 * t, el = (t % 12) / 2;
+    for (int u = 0; u < kScanRays; ++u) {
+        const int head = u / 3, el = (tid >> 7) + 2 * (u % 3);
+        rg[u] = __builtin_nontemporal_load(obs + 48 + (head * 16 + el) * 128 + (tid & 127));
+    }
+}
+
+// onboard_features.cuh:184-234 for one environment, spread over a 256-thread
+// block (6 rays per thread).
+//   * The reference maps non-finite ranges to 0 / +-1000 first; both fail
+//     the 0.35 < r < 11.5 window, as NaN does, so the raw value is tested.
+//   * Pass 1 keeps each ray's corridor centre (x = +inf when the ray is
+//     outside the window or the corridor), so pass 2 is a compare-and-add.
+//   * The closest return is the minimum (range, ray) key: within a thread
+//     rays are visited in increasing index, and the key order breaks range
+//     ties by ray index, so the result is the reference's first minimum in
+//     scan order.  Thread 0 recomputes the winner's world offset with the
+//     same expressions, which gives the values pass 1 formed.
+//   * The frame (attitude rows, py) of this environment was stored one
+//     environment ahead; the last wave stores the next one's between the two
+//     barriers.  Those barriers order every LDS exchange: a slot is rewritten
+//     only after every thread has passed the barrier that follows its reads.
+__device__ __forceinline__ void scan_block(const float (&rg)[kScanRays], const RayPlanes &rays,
+                                           ScanShared &sh, int slot, const float *next_obs,
+                                           int tid, ScanResult &out) {
+    const int lane = tid & 63, w = tid >> 6;
+    float r[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) r[k] = sh.frame[slot][k];
+    const float py = sh.frame[slot][9];
+
+    uint64_t key = kNoReturnKey;
+    float min_dx_c = 30.0f;
+    float xc[kScanRays], yc[kScanRays];
+#pragma unroll
+    for (int u = 0; u < kScanRays; ++u) {
+        const float range = rg[u];
+        xc[u] = __builtin_huge_valf();
+        yc[u] = 0.0f;
+        if (!(range > 0.35f && range < 11.5f)) continue;
+        const int ray = tid + 256 * u;
         const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
         const float rwx = r[0] * dx + r[1] * dy + r[2] * dz;
         const float rwy = r[3] * dx + r[4] * dy + r[5] * dz;
         const float rwz = r[6] * dx + r[7] * dy + r[8] * dz;
-        const float wx = rwx * rg, wy = rwy * rg, wz = rwz * rg;
-        if (el < 4 && rg < best.r) { best.r = rg; best.dx = wx; best.dy = wy; best.ray = ray; }
+        const float wx = rwx * range, wy = rwy * range, wz = rwz * range;
+        // Elevation rows 0..3 are u % 3 < 2 (row (tid >> 7) + 2 (u % 3)).
+        if (u % 3 < 2) {
+            const uint64_t k = (uint64_t)__float_as_uint(range) << 32 | (unsigned)ray;
+            key = k < key ? k : key;
+        }
         const float x_center = wx + rwx * 1.10f;
         const float y_center = py + wy + rwy * 1.10f;
         if (fabsf(wz) <= 2.1f && x_center >= -0.35f && x_center <= 10.5f &&
             fabsf(y_center) <= 3.5f) {
-            xc[t] = x_center;
-            yc[t] = y_center;
+            xc[u] = x_center;
+            yc[u] = y_center;
             min_dx_c = fminf(min_dx_c, x_center);
         }
     }
-    best = wave_key_min(best);
+    key = wave_min_u64(key);
     min_dx_c = wave_min(min_dx_c);
+    if (lane == 0) {
+        sh.key[w] = key;
+        sh.min_dx_c[w] = min_dx_c;
+    }
+    __syncthreads();
+    min_dx_c = sh.min_dx_c[0];
+#pragma unroll
+    for (int k = 1; k < kWavesPerBlock; ++k) min_dx_c = fminf(min_dx_c, sh.min_dx_c[k]);
+    if (w == kWavesPerBlock - 1 && next_obs) store_frame(next_obs, sh.frame[slot ^ 1], lane);
 
     const float limit = min_dx_c + 1.4f;
     int count = 0;
     double y_sum = 0.0;
 #pragma unroll
-    for (int t = 0; t < kRaysPerLane; ++t) {
-        if (xc[t] <= limit) {
+    for (int u = 0; u < kScanRays; ++u) {
+        if (xc[u] <= limit) {
             ++count;
-            y_sum += (double)yc[t];
+            y_sum += (double)yc[u];
         }
     }
     count = wave_sum_int(count);
     y_sum = wave_sum_double(y_sum);
-    out.min_r = best.r;
-    out.min_r_dx = best.dx;
-    out.min_r_dy = best.dy;
-    out.min_ray = best.ray == 0x7fffffff ? -1 : best.ray;
-    out.min_dx_c = min_dx_c;
-    out.cluster_count = count;
-    out.cluster_y_sum = (float)y_sum;
+    if (lane == 0) {
+        sh.count[w] = count;
+        sh.y_sum[w] = y_sum;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        key = sh.key[0];
+        count = sh.count[0];
+        y_sum = sh.y_sum[0];
+#pragma unroll
+        for (int k = 1; k < kWavesPerBlock; ++k) {
+            key = sh.key[k] < key ? sh.key[k] : key;
+            count += sh.count[k];
+            y_sum += sh.y_sum[k];
+        }
+        const int ray = (int)(unsigned)key;
+        const float range = __uint_as_float((unsigned)(key >> 32));
+        out.min_r = range;
+        out.min_r_dx = 0.0f;
+        out.min_r_dy = 0.0f;
+        out.min_ray = -1;
+        if (ray != 0x7fffffff) {
+            const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
+            const float rwx = r[0] * dx + r[1] * dy + r[2] * dz;
+            const float rwy = r[3] * dx + r[4] * dy + r[5] * dz;
+            out.min_r_dx = rwx * range;
+            out.min_r_dy = rwy * range;
+            out.min_ray = ray;
+        }
+        out.min_dx_c = min_dx_c;
+        out.cluster_count = count;
+        out.cluster_y_sum = (float)y_sum;
+    }
 }
 
 // onboard_features.cuh:25-86
@@ -791,26 +867,41 @@ __device__ __forceinline__ void actor_scalars(const float *obs, const float *mis
     }
 }
 
-// Phase 1: one wave per environment scans the LiDAR (persistent blocks share
-// one LDS copy of the ray table).  The 32-byte result is
-// parked in the environment's own prior row (60 bytes), which phase 2 reads
-// before it writes the 15 prior values there: no scratch memory is needed.
+// Phase 1: one 256-thread block per environment scans the LiDAR; blocks
+// are persistent (the ray table is loaded into LDS once per block) and
+// prefetch the next environment's ranges while they scan the current one.
+// The 32-byte result is parked in the environment's own prior row
+// (60 bytes), which phase 2 reads before it writes the 15 prior values
+// there: no scratch memory is needed.
+template <bool SCALARS>
 __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows rows) {
     __shared__ RayPlanes rays;
-    for (int i = threadIdx.x; i < 1536; i += kBlockThreads) {
+    __shared__ ScanShared sh;
+    const int tid = threadIdx.x;
+    size_t env = blockIdx.x;
+    if (env >= rows.batch) return;
+    for (int i = tid; i < 1536; i += kBlockThreads) {
         rays.d[0][i] = kRayDir[i * 3 + 0];
         rays.d[1][i] = kRayDir[i * 3 + 1];
         rays.d[2][i] = kRayDir[i * 3 + 2];
     }
+    const float *first = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
+    if (tid >> 6 == kWavesPerBlock - 1) store_frame(first, sh.frame[0], tid & 63);
+    float rg[kScanRays];
+    load_ranges(first, tid, rg);
     __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    for (size_t env = (size_t)blockIdx.x * kWavesPerBlock + w; env < rows.batch;
-         env += (size_t)gridDim.x * kWavesPerBlock) {
+    for (int slot = 0;; slot ^= 1) {
         const float *obs = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
+        const size_t next = env + gridDim.x;
+        const float *next_obs = next < rows.batch
+            ? reinterpret_cast<const float *>(rows.obs + next * rows.obs_stride) : nullptr;
+        float cur[kScanRays];
+#pragma unroll
+        for (int u = 0; u < kScanRays; ++u) cur[u] = rg[u];
+        if (next_obs) load_ranges(next_obs, tid, rg);
         ScanResult s;
-        scan_lidar(obs, rays, lane, s);
-        if (lane == 0) {
+        scan_block(cur, rays, sh, slot, next_obs, tid, s);
+        if (tid == 0) {
             float *park = rows.prior + env * 15;
             park[0] = s.min_r;
             park[1] = s.min_r_dx;
@@ -820,10 +911,12 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
             park[5] = __int_as_float(s.min_ray);
             park[6] = __int_as_float(s.cluster_count);
         }
-        if (rows.proprio)
+        if (SCALARS && tid < 64)
             actor_scalars(obs,
                           reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride),
-                          lane, rows.proprio + env * 91, rows.mission_vec + env * 49);
+                          tid, rows.proprio + env * 91, rows.mission_vec + env * 49);
+        if (!next_obs) break;
+        env = next;
     }
 }
 
@@ -880,10 +973,12 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
 }
 
 int launch_onboard(const OnboardRows &rows, hipStream_t s) {
-    const size_t scan_want = (rows.batch + kWavesPerBlock - 1) / kWavesPerBlock;
-    const unsigned scan_blocks = scan_want > kScanBlocks ? kScanBlocks : (unsigned)scan_want;
+    const unsigned scan_blocks = rows.batch > kScanBlocks ? kScanBlocks : (unsigned)rows.batch;
     const size_t ctrl_want = (rows.batch + kControlThreads - 1) / kControlThreads;
-    onboard_scan_kernel<<<scan_blocks, kBlockThreads, 0, s>>>(rows);
+    if (rows.proprio)
+        onboard_scan_kernel<true><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
+    else
+        onboard_scan_kernel<false><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
     onboard_control_kernel<<<ctrl_want > kMaxBlocks ? kMaxBlocks : (unsigned)ctrl_want,
                              kControlThreads, 0, s>>>(rows);
     return hipGetLastError() == hipSuccess;
