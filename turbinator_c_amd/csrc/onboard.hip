@@ -214,12 +214,30 @@ struct ScanShared {
     float frame[2][10];  // r[0..8], py
 };
 
+// The observation values the scan frame needs: py = obs[1] and the
+// attitude quaternion obs[6..9].  They are read per lane (the same address
+// in every lane) rather than through the scalar cache, so they travel with
+// the range prefetch and are waited for with it: scalar-cache and LDS
+// completions share one counter, and a scalar load issued early would make
+// every LDS wait of the scan wait for it too.
+struct FrameInputs {
+    float o1, o6, o7, o8, o9;
+};
+
+__device__ __forceinline__ FrameInputs load_frame_inputs(const float *obs) {
+    const int off = __builtin_amdgcn_mbcnt_lo(0u, 0u);  // 0, opaque to the scalarizer
+    return FrameInputs{__builtin_nontemporal_load(obs + 1 + off),
+                       __builtin_nontemporal_load(obs + 6 + off),
+                       __builtin_nontemporal_load(obs + 7 + off),
+                       __builtin_nontemporal_load(obs + 8 + off),
+                       __builtin_nontemporal_load(obs + 9 + off)};
+}
+
 // onboard_features.cuh:105-109,137-145 (attitude) and :183 (py) of one
 // environment, stored for the scan by lane 0 of the calling wave.
-__device__ __forceinline__ void store_frame(const float *obs, float *frame, int lane) {
-    const Attitude att =
-        attitude_of(ob_obs(obs[6]), ob_obs(obs[7]), ob_obs(obs[8]), ob_obs(obs[9]));
-    const float py = ob_obs(obs[1]);
+__device__ __forceinline__ void store_frame(const FrameInputs &in, float *frame, int lane) {
+    const Attitude att = attitude_of(ob_obs(in.o6), ob_obs(in.o7), ob_obs(in.o8), ob_obs(in.o9));
+    const float py = ob_obs(in.o1);
     if (lane == 0) {
 #pragma unroll
         for (int k = 0; k < 9; ++k) frame[k] = att.r[k];
@@ -255,8 +273,9 @@ __device__ __forceinline__ void load_ranges(const float *obs, int tid, float (&r
 //     barriers.  Those barriers order every LDS exchange: a slot is rewritten
 //     only after every thread has passed the barrier that follows its reads.
 __device__ __forceinline__ void scan_block(const float (&rg)[kScanRays], const RayPlanes &rays,
-                                           ScanShared &sh, int slot, const float *next_obs,
-                                           int tid, ScanResult &out) {
+                                           ScanShared &sh, int slot, bool has_next,
+                                           const FrameInputs next_frame, int tid,
+                                           ScanResult &out) {
     const int lane = tid & 63, w = tid >> 6;
     float r[9];
 #pragma unroll
@@ -302,7 +321,7 @@ __device__ __forceinline__ void scan_block(const float (&rg)[kScanRays], const R
     min_dx_c = sh.min_dx_c[0];
 #pragma unroll
     for (int k = 1; k < kWavesPerBlock; ++k) min_dx_c = fminf(min_dx_c, sh.min_dx_c[k]);
-    if (w == kWavesPerBlock - 1 && next_obs) store_frame(next_obs, sh.frame[slot ^ 1], lane);
+    if (w == kWavesPerBlock - 1 && has_next) store_frame(next_frame, sh.frame[slot ^ 1], lane);
 
     const float limit = min_dx_c + 1.4f;
     int count = 0;
@@ -886,7 +905,7 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
         rays.d[2][i] = kRayDir[i * 3 + 2];
     }
     const float *first = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
-    if (tid >> 6 == kWavesPerBlock - 1) store_frame(first, sh.frame[0], tid & 63);
+    if (tid >> 6 == kWavesPerBlock - 1) store_frame(load_frame_inputs(first), sh.frame[0], tid & 63);
     float rg[kScanRays];
     load_ranges(first, tid, rg);
     __syncthreads();
@@ -898,9 +917,18 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
         float cur[kScanRays];
 #pragma unroll
         for (int u = 0; u < kScanRays; ++u) cur[u] = rg[u];
-        if (next_obs) load_ranges(next_obs, tid, rg);
+        // The next environment's frame values and ranges are loaded now.  The
+        // frame values are issued first: the last wave needs them half-way
+        // through this environment, and loads complete in issue order, so
+        // waiting for them does not wait for the ranges, which are used one
+        // environment later.
+        FrameInputs next_in = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if (next_obs) {
+            next_in = load_frame_inputs(next_obs);
+            load_ranges(next_obs, tid, rg);
+        }
         ScanResult s;
-        scan_block(cur, rays, sh, slot, next_obs, tid, s);
+        scan_block(cur, rays, sh, slot, next_obs != nullptr, next_in, tid, s);
         if (tid == 0) {
             float *park = rows.prior + env * 15;
             park[0] = s.min_r;
