@@ -38,7 +38,7 @@ namespace {
 
 constexpr int kBlockThreads = 256;
 constexpr int kWavesPerBlock = kBlockThreads / 64;
-constexpr int kControlThreads = 64;
+constexpr int kControlThreads = 128;  // wave 0 tactical, wave 1 controller
 constexpr int kScanRays = 1536 / kBlockThreads;  // rays per scan thread
 constexpr unsigned kMaxBlocks = 1u << 20;
 constexpr unsigned kScanBlocks = 256 * 8;   // persistent scan grid: 8 per CU
@@ -948,18 +948,39 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
     }
 }
 
-// Phase 2: one thread per environment runs the tactical features and the
-// controller from the parked scan result.  The values are formed in
-// registers and then stored to each destination (the tactical / prior rows
-// and, for the actor, their copies in proprio and mission_vec).  The
-// controller needs ~250 VGPRs, so one wave fills a SIMD: 64-thread blocks
-// spread the 256 waves of a 16,384 batch over every CU instead of a quarter.
+// Phase 2: the tactical features and the controller, from the parked scan
+// result.  They are independent, so a 128-thread block runs them on two
+// waves for the same 64 environments (lane = environment): wave 0 the
+// tactical features, wave 1 the controller.  Each is a long scalar chain
+// (tens of transcendental calls) and only a few waves exist per launch, so
+// splitting the chain shortens the launch and spreads it over twice the
+// SIMDs.  Values are formed in registers and then stored to each
+// destination (the tactical / prior rows and, for the actor, their copies in
+// proprio and mission_vec).
 __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(OnboardRows rows) {
-    for (size_t env = (size_t)blockIdx.x * kControlThreads + threadIdx.x; env < rows.batch;
-         env += (size_t)gridDim.x * kControlThreads) {
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    for (size_t env = (size_t)blockIdx.x * 64 + lane; env < rows.batch;
+         env += (size_t)gridDim.x * 64) {
         const float *obs = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
         const float *mission =
             reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride);
+        if (w == 0) {
+            float t[24];
+            tactical_features(obs, mission, t);
+            float *tac = rows.tactical + env * 24;
+#pragma unroll
+            for (int i = 0; i < 24; ++i) tac[i] = t[i];
+            if (rows.proprio) {
+                float *p = rows.proprio + env * 91, *mv = rows.mission_vec + env * 49;
+#pragma unroll
+                for (int i = 0; i < 24; ++i) {
+                    p[52 + i] = t[i];
+                    mv[10 + i] = t[i];
+                }
+            }
+            continue;
+        }
         float *prior = rows.prior + env * 15;
         ScanResult s;
         s.min_r = prior[0];
@@ -969,21 +990,12 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
         s.cluster_y_sum = prior[4];
         s.min_ray = __float_as_int(prior[5]);
         s.cluster_count = __float_as_int(prior[6]);
-        float t[24], n[15];
-        tactical_features(obs, mission, t);
+        float n[15];
         prior_features(obs, mission, s, n);
-        float *tac = rows.tactical + env * 24;
-#pragma unroll
-        for (int i = 0; i < 24; ++i) tac[i] = t[i];
 #pragma unroll
         for (int i = 0; i < 15; ++i) prior[i] = n[i];
         if (rows.proprio) {
             float *p = rows.proprio + env * 91, *mv = rows.mission_vec + env * 49;
-#pragma unroll
-            for (int i = 0; i < 24; ++i) {
-                p[52 + i] = t[i];
-                mv[10 + i] = t[i];
-            }
 #pragma unroll
             for (int i = 0; i < 15; ++i) {
                 p[76 + i] = n[i];
@@ -1002,7 +1014,7 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
 
 int launch_onboard(const OnboardRows &rows, hipStream_t s) {
     const unsigned scan_blocks = rows.batch > kScanBlocks ? kScanBlocks : (unsigned)rows.batch;
-    const size_t ctrl_want = (rows.batch + kControlThreads - 1) / kControlThreads;
+    const size_t ctrl_want = (rows.batch + 63) / 64;
     if (rows.proprio)
         onboard_scan_kernel<true><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
     else
