@@ -33,7 +33,6 @@ constexpr int kFeatures = 142;
 constexpr int kActions = 15;
 constexpr int kRaw = 2 * kActions;
 constexpr int kFeatureChunks = 9;  // 142 inputs padded to 144
-constexpr int kRounds = 4;         // 16 x 15 (environment, action) slots over 64 lanes
 constexpr int kMinHidden = 16, kMaxHidden = 256;
 constexpr float kPi = 3.14159265358979323846f;
 constexpr size_t kMaxBatch = 0x7fffffffu;
@@ -124,82 +123,98 @@ __device__ __forceinline__ float tanh_hidden(float x) {
     return __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
 }
 
-// One dense layer for the wave's 16 environments: out tile nt = W[tile nt] *
-// in^T + b, fragments as described at the top of the file.  Output tiles are
-// done in groups of up to 8.  The weight chunk of the step after the current
-// one is always in flight while the current chunk runs on the matrix cores
-// (>= 32 MFMAs of 32 cycles, longer than an L2 hit): within a group, into the
-// next group, and from a layer's last step into the next layer's first chunk,
-// which is handed over in `first`.  The bias is loaded when a group starts and
-// added when it ends.  The scheduling barriers keep the compiler from hoisting
-// every load of the layer into registers at once.
-constexpr int kGroup = 8;
+// A workgroup's four waves share one group of 16 environments: in every
+// layer wave w computes output tiles w, w + 4, w + 8, ... (the 142 -> hidden
+// and hidden -> hidden layers) or tile w (the hidden -> 30 layer, waves 0
+// and 1), and the finished tiles go through LDS to all four waves as the next
+// layer's input fragments.  With a 16-environment group per workgroup a
+// 16,384-row batch is 1,024 workgroups, four per CU, so each SIMD holds four
+// waves whose matrix-core work, weight loads and epilogues overlap.
+constexpr int kWaves = 4;
+constexpr int kGroups = 2;  // groups of 16 environments per workgroup pass
 
-template <int KC, int NT, bool TANH, int KCN, int NTN>
-__device__ __forceinline__ void dense_layer(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
-                                            unsigned b_off, unsigned next_w_off,
-                                            const f32x4 (&in)[KC], f32x4 (&out)[NT],
-                                            f32x4 (&first)[kGroup], int lane) {
-    constexpr int G = NT < kGroup ? NT : kGroup;
+// This wave's tiles nt = w + 4j (j < TPW, nt < NT) of one dense layer over
+// KC input chunks, for the workgroup's G groups of 16 environments:
+// out tile = W[tile] * in^T + b.  The layer's input rows are in LDS (`rows`,
+// S floats per environment): lane l reads the B-operand fragment of chunk s,
+// inputs 16s + 4g .. +3 of environment l % 16 of each group, as one float4.
+// Every weight fragment a wave loads feeds 4 G matrix-core steps, one per
+// group, so L2 delivers 1 KiB of weights per 4 G MFMAs.  Weight chunks
+// stream through a ring of kDepth register slots: the chunk of step
+// s + kDepth - 1 is requested while step s runs.  The loop has no branches:
+// a slot j past the layer's tiles (when NT is not a multiple of 4) reads its
+// weights and bias at an offset past the buffer end, which the buffer
+// resource returns as zeros, computes a zero tile and is never stored.  The
+// scheduling barrier keeps the compiler from hoisting every load of the
+// layer.  The per-tile accumulation order (chunk s outer, k-step t inner)
+// does not depend on how tiles or environments are spread over waves.
+constexpr int kDepth = 4;
+constexpr unsigned kPastEnd = 0x80000000u;  // lane offset beyond any packed buffer
+
+template <int KC, int NT, int TPW, int G, bool TANH, int S>
+__device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
+                                            unsigned b_off, const f32x4 *rows,
+                                            f32x4 (&out)[TPW][G], int w, int lane) {
     const int g = lane >> 4;
-    const unsigned wlane = 16u * lane;
-    f32x4 wc[kGroup], wn[kGroup];
+    const f32x4 *in = rows + ((lane & 15) * S) / 4 + g;  // group q, chunk s: in[q 4S + 4 s]
+    unsigned wl[TPW], bl[TPW];
+    int nt[TPW];
 #pragma unroll
-    for (int i = 0; i < kGroup; ++i) wc[i] = first[i];
+    for (int j = 0; j < TPW; ++j) {
+        nt[j] = w + kWaves * j;
+        const bool valid = nt[j] < NT;
+        wl[j] = valid ? 16u * lane : kPastEnd;
+        bl[j] = valid ? 16u * g : kPastEnd;
+        if (!valid) nt[j] = 0;
+    }
+    f32x4 acc[TPW][G], ring[kDepth][TPW], bias[TPW];
 #pragma unroll
-    for (int g0 = 0; g0 < NT; g0 += G) {
-        f32x4 acc[G], bias[G];
+    for (int j = 0; j < TPW; ++j) {
 #pragma unroll
-        for (int i = 0; i < G; ++i)
-            if (g0 + i < NT) {
-                acc[i] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-                bias[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16u * g,
-                                                                b_off + 64u * (g0 + i), 0);
-            }
+        for (int q = 0; q < G; ++q) acc[j][q] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        bias[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, bl[j], b_off + 64u * nt[j], 0);
 #pragma unroll
-        for (int s = 0; s < KC; ++s) {
-            if (s + 1 < KC) {  // next chunk of this group
+        for (int d = 0; d < kDepth - 1; ++d)
+            if (d < KC)
+                ring[d][j] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rsrc, wl[j], w_off + 1024u * (nt[j] * KC + d), 0);
+    }
+    f32x4 xc[G], xn[G];
 #pragma unroll
-                for (int i = 0; i < G; ++i)
-                    if (g0 + i < NT)
-                        wn[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                            rsrc, wlane, w_off + 1024u * ((g0 + i) * KC + s + 1), 0);
-            } else if (g0 + G < NT) {  // first chunk of the next group
+    for (int q = 0; q < G; ++q) xn[q] = xc[q] = in[q * 4 * S];
 #pragma unroll
-                for (int i = 0; i < G; ++i)
-                    if (g0 + G + i < NT)
-                        wn[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                            rsrc, wlane, w_off + 1024u * ((g0 + G + i) * KC), 0);
-            } else if (NTN > 0) {  // first chunk of the next layer
+    for (int s = 0; s < KC; ++s) {
+        if (s + kDepth - 1 < KC) {
 #pragma unroll
-                for (int i = 0; i < kGroup; ++i)
-                    if (i < NTN)
-                        wn[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                            rsrc, wlane, next_w_off + 1024u * (i * KCN), 0);
-            }
+            for (int j = 0; j < TPW; ++j)
+                ring[(s + kDepth - 1) % kDepth][j] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rsrc, wl[j], w_off + 1024u * (nt[j] * KC + s + kDepth - 1), 0);
+        }
+        if (s + 1 < KC) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int i = 0; i < G; ++i)
-                    if (g0 + i < NT)
-                        acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(wc[i][t], in[s][t], acc[i],
-                                                                      0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int i = 0; i < kGroup; ++i) wc[i] = wn[i];
+            for (int q = 0; q < G; ++q) xn[q] = in[q * 4 * S + 4 * (s + 1)];
         }
 #pragma unroll
-        for (int i = 0; i < G; ++i)
-            if (g0 + i < NT) {
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const float y = acc[i][v] + bias[i][v];
-                    out[g0 + i][v] = TANH ? tanh_hidden(y) : y;
-                }
-            }
+            for (int j = 0; j < TPW; ++j)
+#pragma unroll
+                for (int q = 0; q < G; ++q)
+                    acc[j][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        ring[s % kDepth][j][t], xc[q][t], acc[j][q], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < G; ++q) xc[q] = xn[q];
     }
 #pragma unroll
-    for (int i = 0; i < kGroup; ++i) first[i] = wc[i];
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+        for (int q = 0; q < G; ++q)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float y = acc[j][q][v] + bias[j][v];
+                out[j][q][v] = TANH ? tanh_hidden(y) : y;
+            }
 }
 
 __device__ __forceinline__ float finite_or_zero(float x) {  // training.c:61-63
@@ -209,104 +224,150 @@ __device__ __forceinline__ float clampf(float x, float lo, float hi) {  // train
     return x < lo ? lo : (x > hi ? hi : x);
 }
 
-template <int HT>
-__global__ __launch_bounds__(256) void sac_actor_kernel(ActArgs a) {
-    __shared__ float raw_s[4][16][33];
-    __shared__ float term_s[4][16][16];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// Writes this wave's hidden tiles into the workgroup's activation rows: lane
+// l holds outputs 16nt + 4g .. +3 of environment l % 16 of each group, which
+// is exactly the B-operand fragment of input chunk nt of the next layer.
+template <int TPW, int G, int NT, int S>
+__device__ __forceinline__ void store_tiles(f32x4 *rows, const f32x4 (&h)[TPW][G], int w,
+                                            int lane) {
+    const int g = lane >> 4, e = lane & 15;
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+        const int nt = w + kWaves * j;
+        if (nt < NT) {
+#pragma unroll
+            for (int q = 0; q < G; ++q) rows[((16 * q + e) * S) / 4 + 4 * nt + g] = h[j][q];
+        }
+    }
+}
+
+template <int HT, int G>
+__global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
+    constexpr int TPW = (HT + kWaves - 1) / kWaves;  // hidden tiles per wave
+    constexpr int E = 16 * G;                        // environments per workgroup pass
+    // Row stride of the workgroup's LDS rows (floats): the 144 padded
+    // features or the padded hidden activations, plus 4 so rows start on
+    // different banks.  Buffer 1 holds the features during layer 0 and the
+    // second hidden layer afterwards; buffer 0 the first hidden layer.
+    constexpr int S = (16 * HT > 16 * kFeatureChunks ? 16 * HT : 16 * kFeatureChunks) + 4;
+    __shared__ f32x4 buf[2][E * S / 4];
+    __shared__ float raw_s[E][33];
+    __shared__ float term_s[E][16];
+    const int lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, j = lane & 15;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.packed, a.packed_bytes);
-    // Layer 0's first weight chunk; each pass through the layers leaves the
-    // next pass's first chunk here (the last layer prefetches layer 0).
-    f32x4 first[kGroup];
-#pragma unroll
-    for (int i = 0; i < kGroup; ++i)
-        if (i < HT)
-            first[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                wrs, 16u * lane, a.w_off[0] + 1024u * (i * kFeatureChunks), 0);
     // The loop bound is uniform over the block, so every wave meets the
-    // barriers; waves past the batch end compute on zeros and store nothing.
-    for (size_t gbase = (size_t)blockIdx.x * 64; gbase < a.batch;
-         gbase += (size_t)gridDim.x * 64) {
-        const size_t base = gbase + 16 * wave;
-        const size_t env = base + j;
-        const bool live = env < a.batch;
-        // This group's feature rows; rows past the batch end read as zero.
-        const size_t rows = a.batch - gbase < 64 ? a.batch - gbase : 64;
-        const __amdgpu_buffer_rsrc_t frs =
-            make_rsrc(a.features + gbase * kFeatures, (unsigned)(rows * kFeatures * 4));
-        const unsigned frow = (unsigned)(16 * wave + j) * kFeatures * 4;
-        f32x4 x[kFeatureChunks];
+    // barriers; rows past the batch end compute on zeros and store nothing.
+    for (size_t base = (size_t)blockIdx.x * E; base < a.batch; base += (size_t)gridDim.x * E) {
+        // Stage the feature rows in buffer 1 (rows are 568 bytes, 8-byte
+        // aligned): every 8-byte load of the pass is issued before any LDS
+        // store, so the rows arrive in one round trip.  Rows past the batch
+        // end read as zero; inputs 142 and 143 are zero padding.
+        constexpr int kPairs = E * 72;  // 72 float pairs per padded row
+        constexpr int kPerThread = (kPairs + kWaves * 64 - 1) / (kWaves * 64);
+        constexpr int kSlots = (E * kActions + kWaves * 64 - 1) / (kWaves * 64);
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        f32x2 pairs[kPerThread];
+        {
+            const size_t rows = a.batch - base < (size_t)E ? a.batch - base : (size_t)E;
+            const __amdgpu_buffer_rsrc_t frs =
+                make_rsrc(a.features + base * kFeatures, (unsigned)(rows * kFeatures * 4));
 #pragma unroll
-        for (int s = 0; s < kFeatureChunks; ++s) {
-            // Inputs 16s+4g .. +3; rows are 568 bytes, so 8-byte loads stay aligned.
-            const unsigned off = frow + (unsigned)(16 * s + 4 * g) * 4;
-            typedef float f32x2 __attribute__((ext_vector_type(2)));
-            const f32x2 lo = __builtin_bit_cast(
-                f32x2, __builtin_amdgcn_raw_buffer_load_b64(frs, off, 0, 0));
-            f32x2 hi = {0.0f, 0.0f};
-            if (s + 1 < kFeatureChunks || g < 3)  // inputs 142, 143 are padding
-                hi = __builtin_bit_cast(f32x2,
-                                        __builtin_amdgcn_raw_buffer_load_b64(frs, off + 8, 0, 0));
-            x[s] = (f32x4){lo[0], lo[1], hi[0], hi[1]};
-        }
-        // The group's normals (slot p = 15 e + i of environment base + e),
-        // loaded now and used after the three layers.
-        float drawn[kRounds];
-#pragma unroll
-        for (int round = 0; round < kRounds; ++round) {
-            const int p = lane + 64 * round;
-            drawn[round] = 0.0f;
-            if (a.normals && p < 16 * kActions && base + p / kActions < a.batch)
-                drawn[round] = a.normals[base * kActions + p];
-        }
-        f32x4 h0[HT], h1[HT], r[2];
-        dense_layer<kFeatureChunks, HT, true, HT, HT>(wrs, a.w_off[0], a.b_off[0], a.w_off[1], x,
-                                                      h0, first, lane);
-        dense_layer<HT, HT, true, HT, 2>(wrs, a.w_off[1], a.b_off[1], a.w_off[2], h0, h1, first,
-                                         lane);
-        dense_layer<HT, 2, false, kFeatureChunks, (HT < kGroup ? HT : kGroup)>(
-            wrs, a.w_off[2], a.b_off[2], a.w_off[0], h1, r, first, lane);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int n = 16 * nt + 4 * g + v;
-                raw_s[wave][j][n] = r[nt][v];
-                if (a.raw && live && n < kRaw) a.raw[env * kRaw + n] = r[nt][v];
+            for (int it = 0; it < kPerThread; ++it) {
+                const int q = tid + kWaves * 64 * it;
+                const int e = q / 72, k = 2 * (q - 72 * e);
+                pairs[it] = (f32x2){0.0f, 0.0f};
+                if (q < kPairs && k < kFeatures)
+                    pairs[it] = __builtin_bit_cast(
+                        f32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                   frs, (unsigned)(e * kFeatures + k) * 4, 0, 0));
             }
-        __syncthreads();
-        // training.c:310-327 for the wave's 16 x 15 (environment, action)
-        // pairs, consecutive lanes on consecutive action slots.
+        }
+        // The normal draws of this thread's (environment, action) slots
+        // p = tid + 256 r, loaded now and used after the three layers.
+        float drawn[kSlots];
 #pragma unroll
-        for (int round = 0; round < kRounds; ++round) {
-            const int p = lane + 64 * round;
-            const int e = p / kActions, i = p - kActions * e;
-            const size_t ge = base + e;
-            if (p >= 16 * kActions || ge >= a.batch) continue;
-            const float raw_ls = finite_or_zero(raw_s[wave][e][kActions + i]);
+        for (int r = 0; r < kSlots; ++r) {
+            const int p = tid + kWaves * 64 * r;
+            drawn[r] = 0.0f;
+            if (a.normals && p < E * kActions && base + p / kActions < a.batch)
+                drawn[r] = a.normals[base * kActions + p];
+        }
+        {
+            float *xs = reinterpret_cast<float *>(buf[1]);
+#pragma unroll
+            for (int it = 0; it < kPerThread; ++it) {
+                const int q = tid + kWaves * 64 * it;
+                const int e = q / 72, k = 2 * (q - 72 * e);
+                if (q < kPairs) {
+                    xs[e * S + k] = pairs[it][0];
+                    xs[e * S + k + 1] = pairs[it][1];
+                }
+            }
+        }
+        __syncthreads();
+
+        {
+            f32x4 h[TPW][G];
+            layer_tiles<kFeatureChunks, HT, TPW, G, true, S>(wrs, a.w_off[0], a.b_off[0], buf[1],
+                                                             h, w, lane);
+            store_tiles<TPW, G, HT, S>(buf[0], h, w, lane);
+        }
+        __syncthreads();
+        {
+            f32x4 h[TPW][G];
+            layer_tiles<HT, HT, TPW, G, true, S>(wrs, a.w_off[1], a.b_off[1], buf[0], h, w,
+                                                 lane);
+            store_tiles<TPW, G, HT, S>(buf[1], h, w, lane);
+        }
+        __syncthreads();
+        if (w < 2) {
+            f32x4 r[1][G];
+            layer_tiles<HT, 2, 1, G, false, S>(wrs, a.w_off[2], a.b_off[2], buf[1], r, w, lane);
+#pragma unroll
+            for (int q = 0; q < G; ++q) {
+                const size_t env = base + 16 * q + j;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int n = 16 * w + 4 * g + v;
+                    raw_s[16 * q + j][n] = r[0][q][v];
+                    if (a.raw && env < a.batch && n < kRaw) a.raw[env * kRaw + n] = r[0][q][v];
+                }
+            }
+        }
+        __syncthreads();
+        // training.c:310-327 for the E x 15 (environment, action) slots,
+        // consecutive threads on consecutive action slots.
+#pragma unroll
+        for (int r = 0; r < kSlots; ++r) {
+            const int p = tid + kWaves * 64 * r;
+            const int pe = p / kActions, pi = p - kActions * pe;
+            const size_t ge = base + pe;
+            if (p >= E * kActions || ge >= a.batch) continue;
+            const float raw_ls = finite_or_zero(raw_s[pe][kActions + pi]);
             const float log_std = clampf(raw_ls, -3.5f, -1.6f);
             const float sd = expf(log_std);
-            const float eps = a.normals ? drawn[round] * (i == 14 ? 0.15f : 1.0f) : 0.0f;
-            const float z = clampf(finite_or_zero(raw_s[wave][e][i]) + sd * eps, -8.0f, 8.0f);
+            const float eps = a.normals ? drawn[r] * (pi == 14 ? 0.15f : 1.0f) : 0.0f;
+            const float z = clampf(finite_or_zero(raw_s[pe][pi]) + sd * eps, -8.0f, 8.0f);
             const float act = tanhf(z);
-            a.actions[ge * kActions + i] = act;
+            a.actions[ge * kActions + pi] = act;
             const float gaussian = -0.5f * eps * eps - log_std - 0.5f * logf(2.0f * kPi);
-            term_s[wave][e][i] = gaussian - logf(1.0f - act * act + 1.0e-6f);
+            term_s[pe][pi] = gaussian - logf(1.0f - act * act + 1.0e-6f);
         }
         __syncthreads();
-        if (a.log_prob && lane < 16 && base + lane < a.batch) {
+        if (a.log_prob && tid < E && base + tid < a.batch) {
             float lp = 0.0f;  // summed in action order, as the reference does
             if (a.normals)
-                for (int i = 0; i < kActions; ++i) lp += term_s[wave][lane][i];
-            a.log_prob[base + lane] = lp;
+                for (int i = 0; i < kActions; ++i) lp += term_s[tid][i];
+            a.log_prob[base + tid] = lp;
         }
     }
 }
 
 template <int HT>
 void launch_act(const ActArgs &a, unsigned blocks, hipStream_t s) {
-    sac_actor_kernel<HT><<<blocks, 256, 0, s>>>(a);
+    sac_actor_kernel<HT, kGroups><<<blocks, kWaves * 64, 0, s>>>(a);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -366,7 +427,7 @@ extern "C" int tb_hip_sac_actor_act_device(const void *packed, int hidden, const
     a.log_prob = log_prob;
     a.raw = raw;
     a.batch = batch_size;
-    const size_t want = (batch_size + 63) / 64;
+    const size_t want = (batch_size + 16 * kGroups - 1) / (16 * kGroups);
     const unsigned blocks = want > 65536 ? 65536u : (unsigned)want;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     (void)hipGetLastError();
