@@ -358,9 +358,6 @@ def _leg_replay(torch, threads, steps, out):
                        note="bytes_per_env counts only the fused minimum"))
     del r_obs, r_mis, r_cam, g_obs, g_mis, g_cam
 
-    out += host_legs(threads)
-    return out
-
 
 def host_legs(threads: int) -> list:
     """Host-side workloads, PCIe included: the reference's pageable host API
