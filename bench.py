@@ -387,8 +387,11 @@ def host_legs(threads: int) -> list:
     # producer's data already sits in the pinned slots; one slot measures
     # submit + wait latency, two slots the steady state with one batch in
     # flight while the other is collected and resubmitted.
-    for n, slots, reps in ((32, 1, 200), (32, 2, 200), (1024, 1, 20), (1024, 2, 20),
-                           (16384, 2, 6)):
+    for n, slots, reps, direct in ((32, 1, 200, False), (32, 2, 200, False),
+                                   (32, 1, 200, True), (32, 2, 200, True),
+                                   (1024, 1, 20, False), (1024, 2, 20, False),
+                                   (1024, 1, 20, True), (1024, 2, 20, True),
+                                   (16384, 2, 6, False), (16384, 2, 6, True)):
         hb = synth.make_batch(n, seed=9, threads=threads)
         pipe = features.FeaturePipeline.create(0, n, slots)
         assert pipe is not None, "pipeline create failed"
@@ -398,21 +401,22 @@ def host_legs(threads: int) -> list:
                 o[:] = hb.obs
                 m[:] = hb.mission
                 c[:] = hb.cameras
+            submit = pipe.submit_direct if direct else pipe.submit
             for s in range(slots):
-                assert pipe.submit(s, n) == 1, pipe.error()
+                assert submit(s, n) == 1, pipe.error()
                 assert pipe.wait(s, n) is not None, pipe.error()
             t0 = time.perf_counter()
             if slots == 1:
                 for _ in range(reps):
-                    assert pipe.submit(0, n) == 1
+                    assert submit(0, n) == 1
                     assert pipe.wait(0, n) is not None
             else:
                 for s in range(slots):
-                    assert pipe.submit(s, n) == 1
+                    assert submit(s, n) == 1
                 for r in range(reps):
                     s = r % slots
                     assert pipe.wait(s, n) is not None
-                    assert pipe.submit(s, n) == 1
+                    assert submit(s, n) == 1
                 for s in range(slots):
                     assert pipe.wait(s, n) is not None
                 reps += slots
@@ -425,7 +429,9 @@ def host_legs(threads: int) -> list:
             from tests.conftest import assert_feature_parity
             assert_feature_parity(got, oracle.features(hb.obs, hb.mission, hb.cameras),
                                   f"pipeline{n}")
-        out.append(_report(f"pinned pipeline, {n} envs, {slots} slot(s) (PCIe-inclusive)",
+        mode = "direct (kernel on pinned memory)" if direct else "copy engines"
+        out.append(_report(f"pinned pipeline, {mode}, {n} envs, {slots} slot(s) "
+                           "(PCIe-inclusive)",
                            per, n, None,
                            note="producer writes the pinned slots in place; "
                                 + ("submit + wait" if slots == 1 else "steady state, "

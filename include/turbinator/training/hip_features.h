@@ -221,6 +221,14 @@ int tb_hip_feature_pipeline_inputs(tb_hip_feature_pipeline *pipeline, int slot, 
 int tb_hip_feature_pipeline_submit(tb_hip_feature_pipeline *pipeline, int slot, size_t count,
                                    int with_cameras);
 
+/* Like _submit, but the extraction runs on the slot's pinned memory itself:
+ * the kernel reads the inputs over PCIe and writes the features into the
+ * pinned rows that _wait returns, with no copy-engine transfers.  Same
+ * argument and slot-state rules as _submit; 0 with the error set when the
+ * runtime cannot map the slot's pinned memory for the device. */
+int tb_hip_feature_pipeline_submit_direct(tb_hip_feature_pipeline *pipeline, int slot,
+                                          size_t count, int with_cameras);
+
 /* Waits for the slot and returns its feature rows, or NULL (error set) when
  * the slot has never been submitted or the stream failed.  Waiting again on
  * a completed slot returns the same rows. */

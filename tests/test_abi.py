@@ -98,6 +98,7 @@ def test_argument_validation_without_gpu():
     lib.tb_hip_feature_pipeline_destroy(None)
     assert lib.tb_hip_feature_pipeline_inputs(None, 0, None, None, None) == 0
     assert lib.tb_hip_feature_pipeline_submit(None, 0, 1, 1) == 0
+    assert lib.tb_hip_feature_pipeline_submit_direct(None, 0, 1, 1) == 0
     assert not lib.tb_hip_feature_pipeline_wait(None, 0)
 
 

@@ -7,7 +7,9 @@ The pipeline replaces the pageable round trip of the reference host object
 Cases: counts 1, 3, 32 and a full slot (the single-copy path), two slots in
 flight with different data, ten ping-pong rounds with fresh data per round
 (no slot sees another's rows), the no-camera submit, configuration 2
-(1,024 envs) as one full slot, and the slot-state and argument errors.
+(1,024 envs) as one full slot, and the slot-state and argument errors.  The
+direct submit (extraction on the pinned slot itself) gets the same parity
+cases, alternating with copying submits on the same slots.
 Tolerance classes are those of tests/conftest.py.
 """
 from __future__ import annotations
@@ -158,3 +160,58 @@ def test_pipeline_state_and_argument_errors(hip):
         assert pipe.wait(0, 8) is not None
     finally:
         pipe.destroy()   # also drains anything still in flight
+
+
+@pytest.mark.parametrize("count", [1, 32, 200, 256])
+def test_direct_submit_parity(hip, count):
+    note(f"pipeline direct submit, count {count}")
+    pipe = hip.FeaturePipeline.create(0, 256, 2)
+    assert pipe is not None
+    try:
+        b = synth.make_batch(count, seed=500 + count, variant=synth.EDGE_QUARTERS)
+        fill(pipe, 0, b)
+        assert pipe.submit_direct(0, count) == 1, pipe.error()
+        got = pipe.wait(0, count)
+        assert got is not None, pipe.error()
+        assert_feature_parity(got.copy(), oracle.features(b.obs, b.mission, b.cameras),
+                              f"direct{count}")
+        # The same slot through the copying path, then direct again without
+        # cameras: every submit sees only its own rows.
+        c = synth.make_batch(count, seed=600 + count, variant=synth.ORDINARY)
+        fill(pipe, 0, c)
+        assert pipe.submit(0, count) == 1, pipe.error()
+        assert_feature_parity(pipe.wait(0, count).copy(),
+                              oracle.features(c.obs, c.mission, c.cameras), f"copy{count}")
+        assert pipe.submit_direct(0, count, with_cameras=False) == 1, pipe.error()
+        got = pipe.wait(0, count).copy()
+        assert_feature_parity(got, oracle.features(c.obs, c.mission, None), f"direct-nocam{count}")
+        assert pipe.submit_direct(0, count) == 1
+        assert pipe.submit_direct(0, count) == 0
+        assert pipe.error() == "submit: slot 0 is in flight"
+        assert pipe.wait(0, count) is not None
+    finally:
+        pipe.destroy()
+
+
+def test_direct_submit_two_slots_ping_pong(hip):
+    note("pipeline direct submit: ten ping-pong rounds")
+    pipe = hip.FeaturePipeline.create(0, 128, 2)
+    assert pipe is not None
+    try:
+        pending = None
+        for r in range(10):
+            slot, n = r % 2, 64 + 6 * r
+            batch = synth.make_batch(n, seed=2000 + r, variant=synth.ORDINARY)
+            fill(pipe, slot, batch)
+            assert pipe.submit_direct(slot, n) == 1, pipe.error()
+            if pending is not None:
+                pslot, pn, pb = pending
+                assert_feature_parity(pipe.wait(pslot, pn).copy(),
+                                      oracle.features(pb.obs, pb.mission, pb.cameras),
+                                      f"direct-round{r - 1}")
+            pending = (slot, n, batch)
+        pslot, pn, pb = pending
+        assert_feature_parity(pipe.wait(pslot, pn).copy(),
+                              oracle.features(pb.obs, pb.mission, pb.cameras), "direct-round9")
+    finally:
+        pipe.destroy()

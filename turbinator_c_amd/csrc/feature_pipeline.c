@@ -12,6 +12,10 @@
  * and device-to-host copy of one slot on that slot's own stream and returns
  * at once, and a wait hands back the slot's pinned feature rows.  With two
  * slots the next batch is produced while the previous one crosses PCIe.
+ * A direct submit instead runs the extraction on the pinned slot itself:
+ * the kernel reads the inputs over PCIe and writes the features back into
+ * pinned memory, with no copy-engine transfers (the lower-latency choice
+ * for small batches).
  *
  * Layout of one slot, identical in pinned host memory and in device memory
  * (n = max_batch):
@@ -41,6 +45,7 @@ enum {
 typedef struct {
     hipStream_t stream;
     unsigned char *host;    /* pinned, slot layout above */
+    unsigned char *mapped;  /* the same pinned memory as the device addresses it */
     unsigned char *device;  /* device, same layout */
     size_t count;           /* environments of the last submission */
     int in_flight;          /* submitted and not yet waited for */
@@ -94,6 +99,8 @@ tb_hip_feature_pipeline *tb_hip_feature_pipeline_create(int device_id, size_t ma
             tb_hip_feature_pipeline_destroy(p);
             return NULL;
         }
+        if (hipHostGetDevicePointer((void **)&q->mapped, q->host, 0) != hipSuccess)
+            q->mapped = NULL;  /* direct submits report this */
         if (hipMalloc((void **)&q->device, bytes) != hipSuccess) {
             q->device = NULL;
             tb_hip_feature_pipeline_destroy(p);
@@ -170,6 +177,34 @@ int tb_hip_feature_pipeline_submit(tb_hip_feature_pipeline *p, int slot, size_t 
     status = hipMemcpyAsync(q->host + off_features(n), q->device + off_features(n),
                             count * FP_FEATURE_BYTES, hipMemcpyDeviceToHost, q->stream);
     if (status != hipSuccess) return fp_fail(p, "copy features", status);
+    q->count = count;
+    q->in_flight = 1;
+    return 1;
+}
+
+int tb_hip_feature_pipeline_submit_direct(tb_hip_feature_pipeline *p, int slot, size_t count,
+                                          int with_cameras) {
+    if (!fp_valid_slot(p, slot) || count == 0 || count > p->max_batch) return 0;
+    fp_slot *q = &p->slot[slot];
+    if (q->in_flight) {
+        snprintf(p->error, sizeof(p->error), "submit: slot %d is in flight", slot);
+        return 0;
+    }
+    if (!q->mapped) {
+        snprintf(p->error, sizeof(p->error), "submit: slot %d is not device-mapped", slot);
+        return 0;
+    }
+    p->error[0] = 0;
+    const size_t n = p->max_batch;
+    hipError_t status = hipSetDevice(p->device_id);
+    if (status != hipSuccess) return fp_fail(p, "select device", status);
+    q->has_result = 0;
+    if (!tb_cuda_extract_features_device((const float *)q->mapped,
+                                         (const float *)(q->mapped + off_mission(n)),
+                                         with_cameras ? q->mapped + off_cameras(n) : NULL,
+                                         (float *)(q->mapped + off_features(n)), count,
+                                         q->stream))
+        return fp_fail(p, "extract features", hipGetLastError());
     q->count = count;
     q->in_flight = 1;
     return 1;

@@ -186,6 +186,11 @@ class FeaturePipeline:
         return hip_lib().tb_hip_feature_pipeline_submit(self._handle, slot, count,
                                                         1 if with_cameras else 0)
 
+    def submit_direct(self, slot: int, count: int, with_cameras: bool = True) -> int:
+        """Extraction on the pinned slot itself (no copy-engine transfers)."""
+        return hip_lib().tb_hip_feature_pipeline_submit_direct(self._handle, slot, count,
+                                                               1 if with_cameras else 0)
+
     def wait(self, slot: int, count: int) -> np.ndarray | None:
         """The slot's [count,142] pinned feature rows (a view), or None."""
         addr = hip_lib().tb_hip_feature_pipeline_wait(self._handle, slot)

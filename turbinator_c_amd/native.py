@@ -59,6 +59,7 @@ HIP_SIGNATURES = {
     "tb_hip_feature_pipeline_error": (c_char_p, [c_void_p]),
     "tb_hip_feature_pipeline_inputs": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "tb_hip_feature_pipeline_submit": (c_int, [c_void_p, c_int, c_size_t, c_int]),
+    "tb_hip_feature_pipeline_submit_direct": (c_int, [c_void_p, c_int, c_size_t, c_int]),
     "tb_hip_feature_pipeline_wait": (c_void_p, [c_void_p, c_int]),
 }
 
