@@ -39,7 +39,9 @@ namespace {
 constexpr int kBlockThreads = 256;
 constexpr int kWavesPerBlock = kBlockThreads / 64;
 constexpr int kControlThreads = 128;  // wave 0 tactical, wave 1 controller
-constexpr int kScanRays = 1536 / kBlockThreads;  // rays per scan thread
+constexpr int kScanEnvs = 2;                       // environments per scan workgroup pass
+constexpr int kScanThreads = kBlockThreads / kScanEnvs;  // 128 threads per environment
+constexpr int kScanRays = 1536 / kScanThreads;     // 12 rays per thread
 constexpr unsigned kMaxBlocks = 1u << 20;
 constexpr unsigned kScanBlocks = 256 * 8;   // persistent scan grid: 8 per CU
 constexpr size_t kMaxBatch = 0x7fffffffu;
@@ -203,15 +205,15 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
     return swap_min_u64<true>(v);
 }
 
-// Per-wave partial results of one environment's scan, exchanged in LDS, and
-// the attitude rows + lateral position of the environment being scanned and
-// of the next one (written by the block's last wave one environment ahead).
+// Per-wave partial results of the scan, exchanged in LDS, and the attitude
+// rows + lateral position of each environment being scanned and of the next
+// one (written by each environment's last wave one environment ahead).
 struct ScanShared {
     uint64_t key[kWavesPerBlock];
     float min_dx_c[kWavesPerBlock];
     int count[kWavesPerBlock];
     double y_sum[kWavesPerBlock];
-    float frame[2][10];  // r[0..8], py
+    float frame[2][kScanEnvs][10];  // [slot][environment], r[0..8], py
 };
 
 // The observation values the scan frame needs: py = obs[1] and the
@@ -245,42 +247,45 @@ __device__ __forceinline__ void store_frame(const FrameInputs &in, float *frame,
     }
 }
 
-// The six ranges thread `tid` of a scan block owns: rays tid + 256u
-// (u = 0..5), i.e. head u / 3, elevation row (tid >> 7) + 2 (u % 3),
-// azimuth tid & 127.  For each u the block reads 256 consecutive floats
-// (two consecutive LiDAR rows).
-__device__ __forceinline__ void load_ranges(const float *obs, int tid, float (&rg)[kScanRays]) {
+// The twelve ranges thread `sub` (0..127) of an environment's scan threads
+// owns: rays sub + 128u (u = 0..11), i.e. head u / 6, elevation row u % 6,
+// azimuth sub.  For each u the environment's threads read one 512-byte LiDAR
+// row.
+__device__ __forceinline__ void load_ranges(const float *obs, int sub, float (&rg)[kScanRays]) {
 #pragma unroll
-    for (int u = 0; u < kScanRays; ++u) {
-        const int head = u / 3, el = (tid >> 7) + 2 * (u % 3);
-        rg[u] = __builtin_nontemporal_load(obs + 48 + (head * 16 + el) * 128 + (tid & 127));
-    }
+    for (int u = 0; u < kScanRays; ++u)
+        rg[u] = __builtin_nontemporal_load(obs + 48 + (16 * (u / 6) + u % 6) * 128 + sub);
 }
 
-// onboard_features.cuh:184-234 for one environment, spread over a 256-thread
-// block (6 rays per thread).
+// onboard_features.cuh:184-234 for the workgroup's two environments: threads
+// 128h .. 128h + 127 (two waves) scan environment h, 12 rays per thread.
 //   * The reference maps non-finite ranges to 0 / +-1000 first; both fail
 //     the 0.35 < r < 11.5 window, as NaN does, so the raw value is tested.
 //   * Pass 1 keeps each ray's corridor centre (x = +inf when the ray is
 //     outside the window or the corridor), so pass 2 is a compare-and-add.
-//   * The closest return is the minimum (range, ray) key: within a thread
-//     rays are visited in increasing index, and the key order breaks range
-//     ties by ray index, so the result is the reference's first minimum in
-//     scan order.  Thread 0 recomputes the winner's world offset with the
-//     same expressions, which gives the values pass 1 formed.
+//   * The closest return is the minimum (range, ray) key; the key order
+//     breaks range ties by ray index, so the result is the reference's first
+//     minimum in scan order.  Thread 0 of the environment recomputes the
+//     winner's world offset with the same expressions, which gives the
+//     values pass 1 formed.
+//   * Once pass 1 has consumed the ranges, the registers take the next
+//     environment's ranges (`next_obs`, when there is one): they have the
+//     rest of this environment to arrive.
 //   * The frame (attitude rows, py) of this environment was stored one
-//     environment ahead; the last wave stores the next one's between the two
-//     barriers.  Those barriers order every LDS exchange: a slot is rewritten
-//     only after every thread has passed the barrier that follows its reads.
-__device__ __forceinline__ void scan_block(const float (&rg)[kScanRays], const RayPlanes &rays,
-                                           ScanShared &sh, int slot, bool has_next,
-                                           const FrameInputs next_frame, int tid,
-                                           ScanResult &out) {
+//     environment ahead; each environment's last wave stores the next one's
+//     (from `next_frame`) after pass 2, before the second barrier.  Those barriers order
+//     every cross-wave LDS exchange: a slot is rewritten only after every
+//     thread has passed the barrier that follows its reads.
+__device__ __forceinline__ void scan_pair(float (&rg)[kScanRays], const RayPlanes &rays,
+                                          ScanShared &sh, int slot, const float *next_obs,
+                                          bool has_next, const FrameInputs next_frame, int tid,
+                                          ScanResult &out) {
     const int lane = tid & 63, w = tid >> 6;
+    const int h = tid >> 7, sub = tid & 127;
     float r[9];
 #pragma unroll
-    for (int k = 0; k < 9; ++k) r[k] = sh.frame[slot][k];
-    const float py = sh.frame[slot][9];
+    for (int k = 0; k < 9; ++k) r[k] = sh.frame[slot][h][k];
+    const float py = sh.frame[slot][h][9];
 
     uint64_t key = kNoReturnKey;
     float min_dx_c = 30.0f;
@@ -291,14 +296,13 @@ __device__ __forceinline__ void scan_block(const float (&rg)[kScanRays], const R
         xc[u] = __builtin_huge_valf();
         yc[u] = 0.0f;
         if (!(range > 0.35f && range < 11.5f)) continue;
-        const int ray = tid + 256 * u;
+        const int ray = sub + 128 * u;
         const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
         const float rwx = r[0] * dx + r[1] * dy + r[2] * dz;
         const float rwy = r[3] * dx + r[4] * dy + r[5] * dz;
         const float rwz = r[6] * dx + r[7] * dy + r[8] * dz;
         const float wx = rwx * range, wy = rwy * range, wz = rwz * range;
-        // Elevation rows 0..3 are u % 3 < 2 (row (tid >> 7) + 2 (u % 3)).
-        if (u % 3 < 2) {
+        if (u % 6 < 4) {  // elevation rows 0..3
             const uint64_t k = (uint64_t)__float_as_uint(range) << 32 | (unsigned)ray;
             key = k < key ? k : key;
         }
@@ -311,6 +315,8 @@ __device__ __forceinline__ void scan_block(const float (&rg)[kScanRays], const R
             min_dx_c = fminf(min_dx_c, x_center);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    if (next_obs) load_ranges(next_obs, sub, rg);
     key = wave_min_u64(key);
     min_dx_c = wave_min(min_dx_c);
     if (lane == 0) {
@@ -318,10 +324,7 @@ __device__ __forceinline__ void scan_block(const float (&rg)[kScanRays], const R
         sh.min_dx_c[w] = min_dx_c;
     }
     __syncthreads();
-    min_dx_c = sh.min_dx_c[0];
-#pragma unroll
-    for (int k = 1; k < kWavesPerBlock; ++k) min_dx_c = fminf(min_dx_c, sh.min_dx_c[k]);
-    if (w == kWavesPerBlock - 1 && has_next) store_frame(next_frame, sh.frame[slot ^ 1], lane);
+    min_dx_c = fminf(sh.min_dx_c[2 * h], sh.min_dx_c[2 * h + 1]);
 
     const float limit = min_dx_c + 1.4f;
     int count = 0;
@@ -333,6 +336,9 @@ __device__ __forceinline__ void scan_block(const float (&rg)[kScanRays], const R
             y_sum += (double)yc[u];
         }
     }
+    // After pass 2 the corridor values are dead, which leaves the registers
+    // the attitude needs.
+    if ((w & 1) == 1 && has_next) store_frame(next_frame, sh.frame[slot ^ 1][h], lane);
     count = wave_sum_int(count);
     y_sum = wave_sum_double(y_sum);
     if (lane == 0) {
@@ -340,16 +346,11 @@ __device__ __forceinline__ void scan_block(const float (&rg)[kScanRays], const R
         sh.y_sum[w] = y_sum;
     }
     __syncthreads();
-    if (tid == 0) {
-        key = sh.key[0];
-        count = sh.count[0];
-        y_sum = sh.y_sum[0];
-#pragma unroll
-        for (int k = 1; k < kWavesPerBlock; ++k) {
-            key = sh.key[k] < key ? sh.key[k] : key;
-            count += sh.count[k];
-            y_sum += sh.y_sum[k];
-        }
+    if (sub == 0) {
+        const uint64_t k0 = sh.key[2 * h], k1 = sh.key[2 * h + 1];
+        key = k1 < k0 ? k1 : k0;
+        count = sh.count[2 * h] + sh.count[2 * h + 1];
+        y_sum = sh.y_sum[2 * h] + sh.y_sum[2 * h + 1];
         const int ray = (int)(unsigned)key;
         const float range = __uint_as_float((unsigned)(key >> 32));
         out.min_r = range;
@@ -357,9 +358,12 @@ __device__ __forceinline__ void scan_block(const float (&rg)[kScanRays], const R
         out.min_r_dy = 0.0f;
         out.min_ray = -1;
         if (ray != 0x7fffffff) {
+            // The frame slot is rewritten only after the next environment's
+            // pass 2, so it still holds this environment's rows.
+            const float *f = sh.frame[slot][h];
             const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
-            const float rwx = r[0] * dx + r[1] * dy + r[2] * dz;
-            const float rwy = r[3] * dx + r[4] * dy + r[5] * dz;
+            const float rwx = f[0] * dx + f[1] * dy + f[2] * dz;
+            const float rwy = f[3] * dx + f[4] * dy + f[5] * dz;
             out.min_r_dx = rwx * range;
             out.min_r_dy = rwy * range;
             out.min_ray = ray;
@@ -886,50 +890,60 @@ __device__ __forceinline__ void actor_scalars(const float *obs, const float *mis
     }
 }
 
-// Phase 1: one 256-thread block per environment scans the LiDAR; blocks
-// are persistent (the ray table is loaded into LDS once per block) and
-// prefetch the next environment's ranges while they scan the current one.
-// The 32-byte result is parked in the environment's own prior row
-// (60 bytes), which phase 2 reads before it writes the 15 prior values
-// there: no scratch memory is needed.
+// Phase 1: each 256-thread workgroup scans two environments at a time (two
+// waves each); workgroups are persistent (the ray table is loaded into LDS
+// once per workgroup).  The next environment's frame values are requested
+// at the top of each pass and its ranges right after pass 1, both to be
+// used one pass later.  The 32-byte result is parked in the environment's
+// own prior row (60 bytes), which phase 2 reads before it writes the 15
+// prior values there: no scratch memory is needed.
 template <bool SCALARS>
 __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows rows) {
     __shared__ RayPlanes rays;
     __shared__ ScanShared sh;
     const int tid = threadIdx.x;
-    size_t env = blockIdx.x;
-    if (env >= rows.batch) return;
+    const int h = tid >> 7, sub = tid & 127;
+    const size_t stride = (size_t)gridDim.x * kScanEnvs;
+    size_t pair = (size_t)blockIdx.x * kScanEnvs;  // environments pair .. pair + 1
+    if (pair >= rows.batch) return;
     for (int i = tid; i < 1536; i += kBlockThreads) {
         rays.d[0][i] = kRayDir[i * 3 + 0];
         rays.d[1][i] = kRayDir[i * 3 + 1];
         rays.d[2][i] = kRayDir[i * 3 + 2];
     }
-    const float *first = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
-    if (tid >> 6 == kWavesPerBlock - 1) store_frame(load_frame_inputs(first), sh.frame[0], tid & 63);
+    auto obs_of = [&](size_t env) {
+        return reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
+    };
     float rg[kScanRays];
-    load_ranges(first, tid, rg);
+    {
+        const size_t env = pair + h;
+        if (env < rows.batch) {
+            if ((tid >> 6) & 1) store_frame(load_frame_inputs(obs_of(env)), sh.frame[0][h], tid & 63);
+            load_ranges(obs_of(env), sub, rg);
+        } else {
+#pragma unroll
+            for (int u = 0; u < kScanRays; ++u) rg[u] = 0.0f;  // outside the window
+        }
+    }
     __syncthreads();
     for (int slot = 0;; slot ^= 1) {
-        const float *obs = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
-        const size_t next = env + gridDim.x;
-        const float *next_obs = next < rows.batch
-            ? reinterpret_cast<const float *>(rows.obs + next * rows.obs_stride) : nullptr;
-        float cur[kScanRays];
-#pragma unroll
-        for (int u = 0; u < kScanRays; ++u) cur[u] = rg[u];
-        // The next environment's frame values and ranges are loaded now.  The
-        // frame values are issued first: the last wave needs them half-way
-        // through this environment, and loads complete in issue order, so
-        // waiting for them does not wait for the ranges, which are used one
-        // environment later.
+        const size_t env = pair + h;
+        const bool live = env < rows.batch;
+        const size_t next_env = env + stride;
+        const bool has_next = next_env < rows.batch;
+        const float *next_obs = has_next ? obs_of(next_env) : nullptr;
+        // Issued now, used between the barriers: loads complete in issue
+        // order, so that wait does not also cover the range prefetch, which
+        // is issued after pass 1.
         FrameInputs next_in = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        if (next_obs) {
-            next_in = load_frame_inputs(next_obs);
-            load_ranges(next_obs, tid, rg);
-        }
+        if (has_next) next_in = load_frame_inputs(next_obs);
         ScanResult s;
-        scan_block(cur, rays, sh, slot, next_obs != nullptr, next_in, tid, s);
-        if (tid == 0) {
+        scan_pair(rg, rays, sh, slot, next_obs, has_next, next_in, tid, s);
+        if (!has_next) {
+#pragma unroll
+            for (int u = 0; u < kScanRays; ++u) rg[u] = 0.0f;
+        }
+        if (live && sub == 0) {
             float *park = rows.prior + env * 15;
             park[0] = s.min_r;
             park[1] = s.min_r_dx;
@@ -939,12 +953,12 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
             park[5] = __int_as_float(s.min_ray);
             park[6] = __int_as_float(s.cluster_count);
         }
-        if (SCALARS && tid < 64)
-            actor_scalars(obs,
+        if (SCALARS && live && sub < 64)
+            actor_scalars(obs_of(env),
                           reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride),
-                          tid, rows.proprio + env * 91, rows.mission_vec + env * 49);
-        if (!next_obs) break;
-        env = next;
+                          sub, rows.proprio + env * 91, rows.mission_vec + env * 49);
+        pair += stride;
+        if (pair >= rows.batch) break;
     }
 }
 
@@ -1013,7 +1027,8 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
 }
 
 int launch_onboard(const OnboardRows &rows, hipStream_t s) {
-    const unsigned scan_blocks = rows.batch > kScanBlocks ? kScanBlocks : (unsigned)rows.batch;
+    const size_t scan_want = (rows.batch + kScanEnvs - 1) / kScanEnvs;
+    const unsigned scan_blocks = scan_want > kScanBlocks ? kScanBlocks : (unsigned)scan_want;
     const size_t ctrl_want = (rows.batch + 63) / 64;
     if (rows.proprio)
         onboard_scan_kernel<true><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
