@@ -8,15 +8,16 @@
 // the execution shape that suits them:
 //
 //   * the LiDAR scan (two passes over 1,536 rays: closest return, corridor
-//     minimum, cluster membership) runs one wave per environment: lane l owns
-//     rays l + 64t, so each load instruction reads 256 contiguous bytes, and
-//     the scan results are exact wave reductions (lexicographic (range, ray)
-//     minimum = first minimum in the reference scan order) done with DPP and
-//     permlane swaps rather than LDS round trips;
-//   * the scalar controller (mission decode, targets, landing / standard /
-//     inversion / BWB laws, cannon) runs in a second kernel, one thread per
-//     environment, from the scan results (register-heavy code kept apart
-//     from the scan's register-resident ray table, so both keep occupancy).
+//     minimum, cluster membership) runs two waves per environment, 12 rays
+//     per thread, so each load instruction reads contiguous LiDAR rows; the
+//     scan results are exact reductions (the closest return as the minimum
+//     (range, ray) key = first minimum in the reference scan order) done with
+//     DPP and permlane swaps within waves and one LDS exchange between them;
+//   * the tactical features and the scalar controller (mission decode,
+//     targets, landing / standard / inversion / BWB laws, cannon) run in a
+//     second kernel, one lane per environment, from the scan results: the
+//     controller's long register-heavy chain is kept apart from the scan so
+//     both keep their occupancy.
 //
 // Ray directions come from a table generated at build time with the host
 // libm (gen_ray_table.c), and the scan arithmetic is evaluated without FMA

@@ -8,12 +8,13 @@
 //                                        Gaussian action, log-probability
 //
 // The three dense layers run on the matrix cores (v_mfma_f32_16x16x4f32,
-// fp32 in and out).  Each wave owns 16 environments and computes the
-// transposed products  H^T = W * X^T : the weights are the A operand and the
-// environments the columns of B.  With that orientation the 16x16 output
-// fragment a lane holds (outputs 16t+4g..16t+4g+3 of environment lane%16,
-// g = lane/16) is exactly the B-operand fragment the next layer needs for
-// input chunk t, so activations stay in registers from layer to layer.
+// fp32 in and out) as transposed products  H^T = W * X^T  over groups of 16
+// environments: the weights are the A operand and the environments the
+// columns of B.  With that orientation the 16x16 output fragment a lane
+// holds (outputs 16t+4g..16t+4g+3 of environment lane%16, g = lane/16) is
+// exactly the B-operand fragment of input chunk t of the next layer.  A
+// workgroup's four waves split every layer's output tiles between them and
+// pass the finished tiles to each other through LDS in that fragment layout.
 //
 // Weights are first packed (tb_hip_sac_actor_pack_device) into that operand
 // order: for output tile nt, input chunk s (16 inputs) and lane l, one float4
