@@ -441,19 +441,31 @@ def host_legs(threads: int) -> list:
 
 
 def cpu_baseline(host0, threads: int, budget_s: float) -> dict:
-    """The CPU oracle (restatement of src/training/training.c:102-142,
-    -O3 -std=c11) over the first environments of the same batch, on
-    `threads` host threads, repeated until `budget_s` of wall time."""
+    """The reference's own CPU feature twin (src/training/training.c:102-142,
+    compiled from its source into oracle/_ref with its Release flags, -O3
+    -std=c11) over the first environments of the same batch, split over
+    `threads` host threads, repeated until `budget_s` of wall time.  Where
+    oracle/_ref was not built, the oracle's restatement of it is timed
+    instead (kind "port")."""
     import oracle
-    lib = oracle.lib()
+    ref = oracle.ref_lib()
     sample = min(BATCH, 4096 * threads)
     out = np.empty((sample, 142), np.float32)
-    args = (host0.obs.ctypes.data, OBS_B, host0.mission.ctypes.data, MISSION_B,
-            host0.cameras.ctypes.data, CAMERA_B, out.ctypes.data, sample, threads)
-    lib.orc_features_batch(*args)  # warm-up pass
+    if ref is not None:
+        kind = "reference"
+        run = lambda: ref.ref_features_batch(host0.obs.ctypes.data, host0.mission.ctypes.data,  # noqa: E731
+                                             host0.cameras.ctypes.data, out.ctypes.data, sample,
+                                             threads)
+    else:
+        kind = "port"
+        lib = oracle.lib()
+        args = (host0.obs.ctypes.data, OBS_B, host0.mission.ctypes.data, MISSION_B,
+                host0.cameras.ctypes.data, CAMERA_B, out.ctypes.data, sample, threads)
+        run = lambda: lib.orc_features_batch(*args)  # noqa: E731
+    run()  # warm-up pass
     envs, t0 = 0, time.perf_counter()
     while True:
-        lib.orc_features_batch(*args)
+        run()
         envs += sample
         el = time.perf_counter() - t0
         if el >= budget_s:
@@ -467,9 +479,11 @@ def cpu_baseline(host0, threads: int, budget_s: float) -> dict:
                 break
     except OSError:
         pass
-    return {"value": round(rate, 1), "unit": "envs/s", "cores": threads, "kind": "port",
-            "sample": f"{envs} envs ({sample}-env slices of the configuration-3 batch, "
-                      f"{el:.1f} s) on {threads} threads of {cpu}; "
+    what = ("the reference's tb_train_extract_features_cpu" if kind == "reference"
+            else "the oracle restatement of tb_train_extract_features_cpu")
+    return {"value": round(rate, 1), "unit": "envs/s", "cores": threads, "kind": kind,
+            "sample": f"{what} over {envs} envs ({sample}-env slices of the configuration-3 "
+                      f"batch, {el:.1f} s) on {threads} threads of {cpu}; "
                       f"{rate * BYTES_PER_ENV / 1e9:.2f} GB/s effective"}
 
 

@@ -75,6 +75,8 @@ def ref_lib() -> ctypes.CDLL | None:
         l.tb_sac_save.restype = c_int
         l.tb_sac_act_features.argtypes = [c_void_p, c_void_p, c_int, c_void_p, c_void_p]
         l.tb_sac_act_features.restype = c_int
+        l.ref_features_batch.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_int]
+        l.ref_features_batch.restype = None
         _ref = l
     return _ref
 

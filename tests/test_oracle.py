@@ -51,6 +51,25 @@ def test_oracle_matches_compiled_reference(variant):
     assert np.array_equal(got_nocam.view(np.uint32), want_nocam.view(np.uint32))
 
 
+def test_reference_batch_driver_matches_single_calls():
+    """oracle/ref_batch.c (the CPU-baseline driver) returns exactly what the
+    reference's single-environment calls return, for any thread count."""
+    r = oracle.ref_lib()
+    if r is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    b = synth.make_batch(37, seed=77, variant=synth.EDGE_QUARTERS)
+    want = oracle.reference_features(b.obs, b.mission, b.cameras)
+    for threads in (1, 3, 8, 64):
+        out = np.full((37, 142), np.nan, np.float32)
+        r.ref_features_batch(b.obs.ctypes.data, b.mission.ctypes.data, b.cameras.ctypes.data,
+                             out.ctypes.data, 37, threads)
+        assert np.array_equal(out.view(np.uint32), want.view(np.uint32)), threads
+    out = np.full((37, 142), np.nan, np.float32)
+    r.ref_features_batch(b.obs.ctypes.data, b.mission.ctypes.data, None, out.ctypes.data, 37, 4)
+    want_nocam = oracle.reference_features(b.obs, b.mission, None)
+    assert np.array_equal(out.view(np.uint32), want_nocam.view(np.uint32))
+
+
 def test_reference_assertions():
     """tests/test_training.c:25-35 of the reference."""
     obs = np.zeros((1, 4148), np.float32)
