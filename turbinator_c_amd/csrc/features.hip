@@ -227,6 +227,16 @@ __device__ __forceinline__ unsigned min_same_qx(unsigned v) {
     return v;
 }
 
+// Workgroups are dispatched to the 8 XCDs round-robin by id, and each XCD has
+// its own L2.  This bijection of [0, g) gives XCD x the contiguous
+// environments [x n8, (x+1) n8) (n8 = g / 8; ids past 8 n8 map to
+// themselves), so neighbouring environments, whose rows share cache lines at
+// their ends, meet in the same L2.
+__device__ __forceinline__ size_t xcd_contiguous(size_t b, size_t g) {
+    const size_t n8 = g / 8;
+    return b < 8 * n8 ? (b % 8) * n8 + b / 8 : b;
+}
+
 // LV: floats per LiDAR load (4, 2 or 1 from the row alignment).
 // CV: bytes per camera load (16, 8, 4 or 1 from the row alignment).
 // DIAG: also write the per-environment diagnostics (no reference
@@ -257,7 +267,8 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
         unit[k] = chunk * kStagePitch + sector;
     }
 
-    for (size_t env = blockIdx.x; env < rows.batch; env += gridDim.x) {
+    for (size_t env = xcd_contiguous(blockIdx.x, gridDim.x); env < rows.batch;
+         env += gridDim.x) {
         float *out = rows.out + env * kFeatureDim;
         size_t src = env;
         if (rows.index) {
