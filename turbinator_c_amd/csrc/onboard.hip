@@ -8,11 +8,14 @@
 // the execution shape that suits them:
 //
 //   * the LiDAR scan (two passes over 1,536 rays: closest return, corridor
-//     minimum, cluster membership) runs two waves per environment, 12 rays
-//     per thread, so each load instruction reads contiguous LiDAR rows; the
-//     scan results are exact reductions (the closest return as the minimum
+//     minimum, cluster membership) runs one wave per environment, 24 rays
+//     per lane, so each load instruction reads 256 contiguous LiDAR bytes
+//     and no workgroup barrier is needed; the pass over the rays is
+//     branch-free, and the two heads' rays at the same azimuth and elevation
+//     share the first two products of each rotated component; the scan
+//     results are exact reductions (the closest return as the minimum
 //     (range, ray) key = first minimum in the reference scan order) done with
-//     DPP and permlane swaps within waves and one LDS exchange between them;
+//     DPP and permlane swaps, and the cluster count from lane masks;
 //   * the tactical features and the scalar controller (mission decode,
 //     targets, landing / standard / inversion / BWB laws, cannon) run in a
 //     second kernel, one lane per environment, from the scan results: the
@@ -40,11 +43,9 @@ namespace {
 constexpr int kBlockThreads = 256;
 constexpr int kWavesPerBlock = kBlockThreads / 64;
 constexpr int kControlThreads = 128;  // wave 0 tactical, wave 1 controller
-constexpr int kScanEnvs = 2;                       // environments per scan workgroup pass
-constexpr int kScanThreads = kBlockThreads / kScanEnvs;  // 128 threads per environment
-constexpr int kScanRays = 1536 / kScanThreads;     // 12 rays per thread
+constexpr int kScanRays = 1536 / 64;  // rays per lane: one wave scans one environment
 constexpr unsigned kMaxBlocks = 1u << 20;
-constexpr unsigned kScanBlocks = 256 * 8;   // persistent scan grid: 8 per CU
+constexpr unsigned kScanBlocks = 256 * 4;   // persistent scan grid: 4 per CU
 constexpr size_t kMaxBatch = 0x7fffffffu;
 constexpr float kPi = 3.14159265358979323846f;
 
@@ -132,16 +133,6 @@ __device__ __forceinline__ float wave_min(float v) {
     return fminf(a, __int_as_float(o));
 }
 
-__device__ __forceinline__ int wave_sum_int(int v) {
-    v += dpp_partner<0xB1>(v);
-    v += dpp_partner<0x4E>(v);
-    v += dpp_partner<0x141>(v);
-    v += dpp_partner<0x140>(v);
-    int o;
-    v = swap_pair<false>(v, o) + o;
-    return swap_pair<true>(v, o) + o;
-}
-
 __device__ __forceinline__ double wave_sum_double(double v) {
     auto step_dpp = [](double x, auto ctrl_tag) {
         constexpr int C = decltype(ctrl_tag)::value;
@@ -206,152 +197,154 @@ __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
     return swap_min_u64<true>(v);
 }
 
-// Per-wave partial results of the scan, exchanged in LDS, and the attitude
-// rows + lateral position of each environment being scanned and of the next
-// one (written by each environment's last wave one environment ahead).
-struct ScanShared {
-    uint64_t key[kWavesPerBlock];
-    float min_dx_c[kWavesPerBlock];
-    int count[kWavesPerBlock];
-    double y_sum[kWavesPerBlock];
-    float frame[2][kScanEnvs][10];  // [slot][environment], r[0..8], py
+// Buffer resources (gfx9 word 3): loads read zero past num_records instead
+// of faulting, so a resource of 0 bytes turns a prefetch into zeros (ranges
+// outside the scan window) without a branch.  A branch-free prefetch also
+// keeps the load counter exact: a load issued on one path only would make
+// the compiler wait for every load at the join.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr unsigned kObsRowBytes = 4148 * sizeof(float);
+constexpr int kNontemporal = 2;  // cache policy bit 1 (nt)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t obs_rsrc(const float *obs, bool valid) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(obs), (short)0,
+                                             valid ? (int)kObsRowBytes : 0, kBufferWord3);
+}
+
+// The 24 ranges lane l of an environment's wave owns: slot u = 2 row + half
+// is ray 128 row + 64 half + l (row = 6 head + el), so slots run in ray
+// order and each load instruction reads 256 contiguous LiDAR bytes.
+__device__ __forceinline__ void load_ranges(__amdgpu_buffer_rsrc_t obs, int lane,
+                                            float (&rg)[kScanRays]) {
+#pragma unroll
+    for (int u = 0; u < kScanRays; ++u) {
+        const int row = u / 2, head = row / 6, el = row % 6;
+        rg[u] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(
+                       obs, 4 * (48 + lane), 4 * ((16 * head + el) * 128 + 64 * (u % 2)),
+                       kNontemporal));
+    }
+}
+
+// onboard_features.cuh:105-109,137-145 (attitude rows) and :183 (py) of one
+// environment: the frame of its scan.
+struct ScanFrame {
+    float r[9], py;
 };
 
-// The observation values the scan frame needs: py = obs[1] and the
-// attitude quaternion obs[6..9].  They are read per lane (the same address
-// in every lane) rather than through the scalar cache, so they travel with
-// the range prefetch and are waited for with it: scalar-cache and LDS
-// completions share one counter, and a scalar load issued early would make
-// every LDS wait of the scan wait for it too.
-struct FrameInputs {
+struct FrameObs {
     float o1, o6, o7, o8, o9;
 };
 
-__device__ __forceinline__ FrameInputs load_frame_inputs(const float *obs) {
-    const int off = __builtin_amdgcn_mbcnt_lo(0u, 0u);  // 0, opaque to the scalarizer
-    return FrameInputs{__builtin_nontemporal_load(obs + 1 + off),
-                       __builtin_nontemporal_load(obs + 6 + off),
-                       __builtin_nontemporal_load(obs + 7 + off),
-                       __builtin_nontemporal_load(obs + 8 + off),
-                       __builtin_nontemporal_load(obs + 9 + off)};
+__device__ __forceinline__ FrameObs load_frame_obs(const float *obs) {
+    return FrameObs{obs[1], obs[6], obs[7], obs[8], obs[9]};
 }
 
-// onboard_features.cuh:105-109,137-145 (attitude) and :183 (py) of one
-// environment, stored for the scan by lane 0 of the calling wave.
-__device__ __forceinline__ void store_frame(const FrameInputs &in, float *frame, int lane) {
-    const Attitude att = attitude_of(ob_obs(in.o6), ob_obs(in.o7), ob_obs(in.o8), ob_obs(in.o9));
-    const float py = ob_obs(in.o1);
-    if (lane == 0) {
+__device__ __forceinline__ ScanFrame scan_frame(FrameObs v) {
+    // An empty asm that takes the five values waits for their loads once,
+    // here, instead of letting each load sink to its use inside the branchy
+    // non-finite mapping (one memory round trip each).
+    asm volatile("" : "+v"(v.o1), "+v"(v.o6), "+v"(v.o7), "+v"(v.o8), "+v"(v.o9));
+    const Attitude att = attitude_of(ob_obs(v.o6), ob_obs(v.o7), ob_obs(v.o8), ob_obs(v.o9));
+    ScanFrame f;
 #pragma unroll
-        for (int k = 0; k < 9; ++k) frame[k] = att.r[k];
-        frame[9] = py;
-    }
+    for (int k = 0; k < 9; ++k) f.r[k] = att.r[k];
+    f.py = ob_obs(v.o1);
+    return f;
 }
 
-// The twelve ranges thread `sub` (0..127) of an environment's scan threads
-// owns: rays sub + 128u (u = 0..11), i.e. head u / 6, elevation row u % 6,
-// azimuth sub.  For each u the environment's threads read one 512-byte LiDAR
-// row.
-__device__ __forceinline__ void load_ranges(const float *obs, int sub, float (&rg)[kScanRays]) {
-#pragma unroll
-    for (int u = 0; u < kScanRays; ++u)
-        rg[u] = __builtin_nontemporal_load(obs + 48 + (16 * (u / 6) + u % 6) * 128 + sub);
-}
-
-// onboard_features.cuh:184-234 for the workgroup's two environments: threads
-// 128h .. 128h + 127 (two waves) scan environment h, 12 rays per thread.
+// onboard_features.cuh:184-234 for one environment, on one wave (24 rays per
+// lane, no workgroup barrier).
 //   * The reference maps non-finite ranges to 0 / +-1000 first; both fail
 //     the 0.35 < r < 11.5 window, as NaN does, so the raw value is tested.
-//   * Pass 1 keeps each ray's corridor centre (x = +inf when the ray is
+//   * The closest return is the minimum (range, ray) key over elevation rows
+//     0..3: the key order breaks range ties by ray index, so the result is
+//     the reference's first minimum in scan order.  Lane 0 recomputes the
+//     winner's world offset with the reference's expression, which gives the
+//     value pass 1 formed (see the pair identity below).
+//   * Pass 1 is branch-free and keeps each ray's corridor centre (x = +inf
 //     outside the window or the corridor), so pass 2 is a compare-and-add.
-//   * The closest return is the minimum (range, ray) key; the key order
-//     breaks range ties by ray index, so the result is the reference's first
-//     minimum in scan order.  Thread 0 of the environment recomputes the
-//     winner's world offset with the same expressions, which gives the
-//     values pass 1 formed.
 //   * Once pass 1 has consumed the ranges, the registers take the next
-//     environment's ranges (`next_obs`, when there is one): they have the
-//     rest of this environment to arrive.
-//   * The frame (attitude rows, py) of this environment was stored one
-//     environment ahead; each environment's last wave stores the next one's
-//     (from `next_frame`) after pass 2, before the second barrier.  Those barriers order
-//     every cross-wave LDS exchange: a slot is rewritten only after every
-//     thread has passed the barrier that follows its reads.
-__device__ __forceinline__ void scan_pair(float (&rg)[kScanRays], const RayPlanes &rays,
-                                          ScanShared &sh, int slot, const float *next_obs,
-                                          bool has_next, const FrameInputs next_frame, int tid,
-                                          ScanResult &out) {
-    const int lane = tid & 63, w = tid >> 6;
-    const int h = tid >> 7, sub = tid & 127;
-    float r[9];
+//     environment's (`next`, a 0-byte resource when there is none): they
+//     have the rest of this environment to arrive.
+//   * `f` is wave-uniform.
+__device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes &rays,
+                                         const ScanFrame &f, __amdgpu_buffer_rsrc_t next,
+                                         int lane, ScanResult &out) {
+    // Closest-return candidate of this lane, in ray order (strict <).
+    // Starting the running best at 11.5 folds the window's upper bound into
+    // that compare.
+    float best_r = 11.5f;
+    int best_u = -1;
 #pragma unroll
-    for (int k = 0; k < 9; ++k) r[k] = sh.frame[slot][h][k];
-    const float py = sh.frame[slot][h][9];
-
+    for (int u = 0; u < kScanRays; ++u) {
+        if ((u / 2) % 6 >= 4) continue;
+        const bool take = (int)(rg[u] > 0.35f) & (int)(rg[u] < best_r);
+        best_r = take ? rg[u] : best_r;
+        best_u = take ? u : best_u;
+    }
     uint64_t key = kNoReturnKey;
+    if (best_u >= 0)
+        key = (uint64_t)__float_as_uint(best_r) << 32 | (unsigned)(64 * best_u + lane);
+
+    // Pass 1.  The rays of rows el and el + 6 (heads 0 and 1) at the same
+    // azimuth have the same table x, y and the negated z, bit for bit.  With
+    // the reference's order (R0 d.x + R1 d.y) + R2 d.z the head-1 sum is
+    // therefore P - Q where the head-0 sum is P + Q, exactly (a + (-b) and
+    // a - b are the same IEEE operation), so each pair reads one direction
+    // and forms P and Q once.
     float min_dx_c = 30.0f;
     float xc[kScanRays], yc[kScanRays];
 #pragma unroll
-    for (int u = 0; u < kScanRays; ++u) {
-        const float range = rg[u];
-        xc[u] = __builtin_huge_valf();
-        yc[u] = 0.0f;
-        if (!(range > 0.35f && range < 11.5f)) continue;
-        const int ray = sub + 128 * u;
-        const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
-        const float rwx = r[0] * dx + r[1] * dy + r[2] * dz;
-        const float rwy = r[3] * dx + r[4] * dy + r[5] * dz;
-        const float rwz = r[6] * dx + r[7] * dy + r[8] * dz;
-        const float wx = rwx * range, wy = rwy * range, wz = rwz * range;
-        if (u % 6 < 4) {  // elevation rows 0..3
-            const uint64_t k = (uint64_t)__float_as_uint(range) << 32 | (unsigned)ray;
-            key = k < key ? k : key;
-        }
-        const float x_center = wx + rwx * 1.10f;
-        const float y_center = py + wy + rwy * 1.10f;
-        if (fabsf(wz) <= 2.1f && x_center >= -0.35f && x_center <= 10.5f &&
-            fabsf(y_center) <= 3.5f) {
-            xc[u] = x_center;
-            yc[u] = y_center;
-            min_dx_c = fminf(min_dx_c, x_center);
+    for (int el = 0; el < 6; ++el) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int ray = 128 * el + 64 * half + lane;
+            const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
+            const float p0 = f.r[0] * dx + f.r[1] * dy, q0 = f.r[2] * dz;
+            const float p1 = f.r[3] * dx + f.r[4] * dy, q1 = f.r[5] * dz;
+            const float p2 = f.r[6] * dx + f.r[7] * dy, q2 = f.r[8] * dz;
+#pragma unroll
+            for (int head = 0; head < 2; ++head) {
+                const int u = 2 * (6 * head + el) + half;
+                const float range = rg[u];
+                const float rwx = head ? p0 - q0 : p0 + q0;
+                const float rwy = head ? p1 - q1 : p1 + q1;
+                const float rwz = head ? p2 - q2 : p2 + q2;
+                const float wx = rwx * range, wy = rwy * range, wz = rwz * range;
+                const float x_center = wx + rwx * 1.10f;
+                const float y_center = f.py + wy + rwy * 1.10f;
+                // Bitwise, so the compares stay one straight-line block.
+                const bool corridor = (int)(range > 0.35f) & (int)(range < 11.5f) &
+                                      (int)(fabsf(wz) <= 2.1f) & (int)(x_center >= -0.35f) &
+                                      (int)(x_center <= 10.5f) & (int)(fabsf(y_center) <= 3.5f);
+                xc[u] = corridor ? x_center : __builtin_huge_valf();
+                yc[u] = y_center;
+                min_dx_c = (int)corridor & (int)(x_center < min_dx_c) ? x_center : min_dx_c;
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (next_obs) load_ranges(next_obs, sub, rg);
+    load_ranges(next, lane, rg);
     key = wave_min_u64(key);
     min_dx_c = wave_min(min_dx_c);
-    if (lane == 0) {
-        sh.key[w] = key;
-        sh.min_dx_c[w] = min_dx_c;
-    }
-    __syncthreads();
-    min_dx_c = fminf(sh.min_dx_c[2 * h], sh.min_dx_c[2 * h + 1]);
 
+    // Pass 2: the cluster is counted from the lane masks (scalar unit); y is
+    // summed in double.  Adding +0.0 for the rays outside the cluster leaves
+    // the sum unchanged: it starts at +0.0 and never becomes -0.0.
     const float limit = min_dx_c + 1.4f;
     int count = 0;
     double y_sum = 0.0;
 #pragma unroll
     for (int u = 0; u < kScanRays; ++u) {
-        if (xc[u] <= limit) {
-            ++count;
-            y_sum += (double)yc[u];
-        }
+        const bool in = xc[u] <= limit;
+        count += __builtin_popcountll(__builtin_amdgcn_ballot_w64(in));
+        float y = in ? yc[u] : 0.0f;
+        asm("" : "+v"(y));  // select the float, then widen (one select, not two)
+        y_sum += (double)y;
     }
-    // After pass 2 the corridor values are dead, which leaves the registers
-    // the attitude needs.
-    if ((w & 1) == 1 && has_next) store_frame(next_frame, sh.frame[slot ^ 1][h], lane);
-    count = wave_sum_int(count);
     y_sum = wave_sum_double(y_sum);
     if (lane == 0) {
-        sh.count[w] = count;
-        sh.y_sum[w] = y_sum;
-    }
-    __syncthreads();
-    if (sub == 0) {
-        const uint64_t k0 = sh.key[2 * h], k1 = sh.key[2 * h + 1];
-        key = k1 < k0 ? k1 : k0;
-        count = sh.count[2 * h] + sh.count[2 * h + 1];
-        y_sum = sh.y_sum[2 * h] + sh.y_sum[2 * h + 1];
         const int ray = (int)(unsigned)key;
         const float range = __uint_as_float((unsigned)(key >> 32));
         out.min_r = range;
@@ -359,12 +352,9 @@ __device__ __forceinline__ void scan_pair(float (&rg)[kScanRays], const RayPlane
         out.min_r_dy = 0.0f;
         out.min_ray = -1;
         if (ray != 0x7fffffff) {
-            // The frame slot is rewritten only after the next environment's
-            // pass 2, so it still holds this environment's rows.
-            const float *f = sh.frame[slot][h];
             const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
-            const float rwx = f[0] * dx + f[1] * dy + f[2] * dz;
-            const float rwy = f[3] * dx + f[4] * dy + f[5] * dz;
+            const float rwx = f.r[0] * dx + f.r[1] * dy + f.r[2] * dz;
+            const float rwy = f.r[3] * dx + f.r[4] * dy + f.r[5] * dz;
             out.min_r_dx = rwx * range;
             out.min_r_dy = rwy * range;
             out.min_ray = ray;
@@ -891,60 +881,56 @@ __device__ __forceinline__ void actor_scalars(const float *obs, const float *mis
     }
 }
 
-// Phase 1: each 256-thread workgroup scans two environments at a time (two
-// waves each); workgroups are persistent (the ray table is loaded into LDS
-// once per workgroup).  The next environment's frame values are requested
-// at the top of each pass and its ranges right after pass 1, both to be
-// used one pass later.  The 32-byte result is parked in the environment's
-// own prior row (60 bytes), which phase 2 reads before it writes the 15
-// prior values there: no scratch memory is needed.
+// Phase 1: each wave scans one environment at a time; workgroups are
+// persistent (the ray table is loaded into LDS once per workgroup, the only
+// barrier).  Wave g of the grid takes environments g, g + W, g + 2W, ...
+// (W waves in the grid).  Their scan frames (attitude rows, py) are formed
+// up front, lane j for the wave's j-th environment, and each environment's
+// frame is then read from its lane into scalar registers.  Each
+// environment's ranges are requested while the previous one finishes.  The
+// 32-byte result is parked in the environment's own prior row (60 bytes),
+// which phase 2 reads before it writes the 15 prior values there: no
+// scratch memory is needed.
 template <bool SCALARS>
 __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows rows) {
     __shared__ RayPlanes rays;
-    __shared__ ScanShared sh;
-    const int tid = threadIdx.x;
-    const int h = tid >> 7, sub = tid & 127;
-    const size_t stride = (size_t)gridDim.x * kScanEnvs;
-    size_t pair = (size_t)blockIdx.x * kScanEnvs;  // environments pair .. pair + 1
-    if (pair >= rows.batch) return;
+    const int tid = threadIdx.x, lane = tid & 63;
     for (int i = tid; i < 1536; i += kBlockThreads) {
         rays.d[0][i] = kRayDir[i * 3 + 0];
         rays.d[1][i] = kRayDir[i * 3 + 1];
         rays.d[2][i] = kRayDir[i * 3 + 2];
     }
-    auto obs_of = [&](size_t env) {
-        return reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
-    };
-    float rg[kScanRays];
-    {
-        const size_t env = pair + h;
-        if (env < rows.batch) {
-            if ((tid >> 6) & 1) store_frame(load_frame_inputs(obs_of(env)), sh.frame[0][h], tid & 63);
-            load_ranges(obs_of(env), sub, rg);
-        } else {
-#pragma unroll
-            for (int u = 0; u < kScanRays; ++u) rg[u] = 0.0f;  // outside the window
-        }
-    }
     __syncthreads();
-    for (int slot = 0;; slot ^= 1) {
-        const size_t env = pair + h;
-        const bool live = env < rows.batch;
-        const size_t next_env = env + stride;
-        const bool has_next = next_env < rows.batch;
-        const float *next_obs = has_next ? obs_of(next_env) : nullptr;
-        // Issued now, used between the barriers: loads complete in issue
-        // order, so that wait does not also cover the range prefetch, which
-        // is issued after pass 1.
-        FrameInputs next_in = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        if (has_next) next_in = load_frame_inputs(next_obs);
-        ScanResult s;
-        scan_pair(rg, rays, sh, slot, next_obs, has_next, next_in, tid, s);
-        if (!has_next) {
+    const size_t waves = (size_t)gridDim.x * kWavesPerBlock;
+    size_t env = (size_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (env >= rows.batch) return;
+    auto obs_of = [&](size_t e) {
+        return reinterpret_cast<const float *>(rows.obs + e * rows.obs_stride);
+    };
+    // Lane j forms the frame of the wave's j-th environment from here (a
+    // lane past the batch repeats the current one, whose row exists).
+    auto frame_obs = [&](size_t first) {
+        const size_t e = first + (size_t)lane * waves;
+        return load_frame_obs(obs_of(e < rows.batch ? e : first));
+    };
+    const FrameObs first_obs = frame_obs(env);
+    float rg[kScanRays];
+    load_ranges(obs_rsrc(obs_of(env), true), lane, rg);
+    ScanFrame mine = scan_frame(first_obs);
+    for (int k = 0;;) {
+        ScanFrame f;
 #pragma unroll
-            for (int u = 0; u < kScanRays; ++u) rg[u] = 0.0f;
-        }
-        if (live && sub == 0) {
+        for (int i = 0; i < 9; ++i)
+            f.r[i] = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine.r[i]), k));
+        f.py = __builtin_bit_cast(float,
+                                  __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine.py), k));
+        const size_t next_env = env + waves;
+        const bool has_next = next_env < rows.batch;
+        ScanResult s;
+        scan_env(rg, rays, f, obs_rsrc(has_next ? obs_of(next_env) : nullptr, has_next), lane,
+                 s);
+        if (lane == 0) {
             float *park = rows.prior + env * 15;
             park[0] = s.min_r;
             park[1] = s.min_r_dx;
@@ -954,12 +940,16 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
             park[5] = __int_as_float(s.min_ray);
             park[6] = __int_as_float(s.cluster_count);
         }
-        if (SCALARS && live && sub < 64)
+        if (SCALARS)
             actor_scalars(obs_of(env),
                           reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride),
-                          sub, rows.proprio + env * 91, rows.mission_vec + env * 49);
-        pair += stride;
-        if (pair >= rows.batch) break;
+                          lane, rows.proprio + env * 91, rows.mission_vec + env * 49);
+        if (!has_next) break;
+        env = next_env;
+        if (++k == 64) {  // the next 64 environments of this wave
+            k = 0;
+            mine = scan_frame(frame_obs(env));
+        }
     }
 }
 
@@ -1028,7 +1018,7 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
 }
 
 int launch_onboard(const OnboardRows &rows, hipStream_t s) {
-    const size_t scan_want = (rows.batch + kScanEnvs - 1) / kScanEnvs;
+    const size_t scan_want = (rows.batch + kWavesPerBlock - 1) / kWavesPerBlock;
     const unsigned scan_blocks = scan_want > kScanBlocks ? kScanBlocks : (unsigned)scan_want;
     const size_t ctrl_want = (rows.batch + 63) / 64;
     if (rows.proprio)
