@@ -106,10 +106,23 @@ def build_oracle() -> None:
     _run(["make", "-s", "-C", str(ROOT / "oracle"), "all"])
 
 
+GPU_CHECKS = ROOT / "tests" / "csrc"
+GPU_CHECK_BIN = GPU_CHECKS / "bin"
+
+
+def build_gpu_checks() -> None:
+    """Stand-alone gfx950 probes the GPU tests run (tests/csrc/*.hip)."""
+    GPU_CHECK_BIN.mkdir(exist_ok=True)
+    for src in sorted(GPU_CHECKS.glob("*.hip")):
+        exe = GPU_CHECK_BIN / src.stem
+        _run([hipcc(), *HIP_FLAGS, "-o", str(exe), str(src)])
+
+
 def build_all() -> None:
     build_synth_library()
     build_oracle()
     build_hip_library()
+    build_gpu_checks()
 
 
 if __name__ == "__main__":

@@ -65,9 +65,20 @@ __device__ __forceinline__ float ob_obs(float x) {
 __device__ __forceinline__ float ob_mission(float x) {
     return __builtin_isnan(x) ? 0.0f : (__builtin_isinf(x) ? copysignf(1.0f, x) : x);
 }
+// sinf and cosf of one argument through sincosf: one argument reduction
+// instead of two, and the same bits as the separate calls for every float
+// (checked over all 2^32 inputs on gfx950 by tests/csrc/check_sincos.hip).
+struct SinCos {
+    float s, c;
+};
+__device__ __forceinline__ SinCos sin_cos(float x) {
+    SinCos r;
+    sincosf(x, &r.s, &r.c);
+    return r;
+}
 __device__ __forceinline__ float ob_wrap(float target, float current) {
-    const float d = target - current;
-    return atan2f(sinf(d), cosf(d));
+    const SinCos d = sin_cos(target - current);
+    return atan2f(d.s, d.c);
 }
 __device__ __forceinline__ float ob_norm3(float x, float y, float z) {
     return sqrtf(x * x + y * y + z * z);
@@ -392,7 +403,9 @@ __device__ void tactical_features(const float *o, const float *m, float *t) {
     const float ct = ob_clamp(1.0f - 2.0f * (qx * qx + qy * qy), -1.0f, 1.0f);
     const float bx_x = 1.0f - 2.0f * (qy * qy + qz * qz);
     const float bx_y = 2.0f * (qx * qy + qw * qz);
-    const float yaw = atan2f(bx_y, bx_x), cy = cosf(yaw), sy = sinf(yaw);
+    const float yaw = atan2f(bx_y, bx_x);
+    const SinCos yaw_sc = sin_cos(yaw);
+    const float cy = yaw_sc.c, sy = yaw_sc.s;
     v[8] = cy * bz_y - sy * bz_x;
     v[9] = -sy * bz_y - cy * bz_x;
     v[10] = ct;
@@ -468,8 +481,10 @@ __device__ void prior_features(const float *input_obs, const float *input_missio
         thrust[i] = max_installed * (idle_frac + (1.0f - idle_frac) * spool[i]);
         outer[i] = atan2f(o[20 + i], o[24 + i]);
         const float inner = o[28 + i];
-        fz[i] = thrust[i] * cosf(outer[i]) * cosf(inner);
-        ft[i] = thrust[i] * sinf(outer[i]) * cosf(inner);
+        const SinCos o_sc = sin_cos(outer[i]);
+        const float c_inner = cosf(inner);
+        fz[i] = thrust[i] * o_sc.c * c_inner;
+        ft[i] = thrust[i] * o_sc.s * c_inner;
         total_fz += fz[i];
         jammed_yaw_ft += ft[i];
     }
@@ -530,8 +545,9 @@ __device__ void prior_features(const float *input_obs, const float *input_missio
     float avoid_x = 0.0f, avoid_y = 0.0f, slalom_speed = 3.8f, nearest_dx = 30.0f;
     if (dodge && scan.min_r < 7.5f) {
         const float min_az = atan2f(scan.min_r_dy, scan.min_r_dx);
-        avoid_x = -sinf(min_az) * 2.2f;
-        avoid_y = cosf(min_az) * 2.2f;
+        const SinCos az = sin_cos(min_az);
+        avoid_x = -az.s * 2.2f;
+        avoid_y = az.c * 2.2f;
     }
     const float min_dx_c = scan.min_dx_c;
     const int cluster_count = scan.cluster_count;
@@ -632,7 +648,8 @@ __device__ void prior_features(const float *input_obs, const float *input_missio
         (mass * des_ax + damp_v * vx - tilt_comp * total_fz * body_z_x) * horiz_scale;
     const float fy_world =
         (mass * des_ay + damp_v * vy - tilt_comp * total_fz * body_z_y) * horiz_scale;
-    const float cyaw = cosf(yaw), syaw = sinf(yaw);
+    const SinCos yaw_sc = sin_cos(yaw);
+    const float cyaw = yaw_sc.c, syaw = yaw_sc.s;
     const float max_fh =
         active_slalom ? 105.0f : (lateral ? 125.0f : (heavy_cargo ? 52.0f : 80.0f));
     const float fx_body = ob_clamp(cyaw * fx_world + syaw * fy_world, -max_fh, max_fh);
@@ -781,7 +798,8 @@ __device__ void prior_features(const float *input_obs, const float *input_missio
         const float pitch_up = asinf(ob_clamp(r20, -1.0f, 1.0f));
         const float climb_des = ob_clamp(0.42f * gz, -5.0f, 5.0f);
         const float climb_err = climb_des - vz;
-        const float cos_bank = cosf(roll_right), sin_bank = sinf(roll_right);
+        const SinCos bank = sin_cos(roll_right);
+        const float cos_bank = bank.c, sin_bank = bank.s;
         const float gamma_des = atan2f(climb_des, fmaxf(gs, 14.0f));
         float desired_pitch = ob_clamp(0.062831853f + 0.75f * gamma_des + 0.035f * climb_err +
                                            0.09f * (1.0f - fmaxf(cos_bank, 0.5f)),
