@@ -42,7 +42,7 @@ namespace {
 
 constexpr int kBlockThreads = 256;
 constexpr int kWavesPerBlock = kBlockThreads / 64;
-constexpr int kControlThreads = 128;  // wave 0 tactical, wave 1 controller
+constexpr int kControlThreads = 320;  // wave 0 tactical, waves 1..4 controller
 constexpr int kScanRays = 1536 / 64;  // rays per lane: one wave scans one environment
 constexpr unsigned kMaxBlocks = 1u << 20;
 constexpr unsigned kScanBlocks = 256 * 4;   // persistent scan grid: 4 per CU
@@ -446,9 +446,27 @@ __device__ void tactical_features(const float *o, const float *m, float *t) {
                                      : (__builtin_isinf(v[i]) ? copysignf(1.0f, v[i]) : v[i]);
 }
 
-// onboard_features.cuh:88-513 with the LiDAR passes replaced by `scan`.
-__device__ void prior_features(const float *input_obs, const float *input_mission,
-                               const ScanResult &scan, float *n) {
+// Lane k of every group of four (a quad) reads quad lane K's value.
+template <int K>
+__device__ __forceinline__ float quad_lane(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xF, 0xF, false));
+}
+
+// One lane's share of the prior features: its arm's throttle, outer and
+// inner commands, and (identical in the four lanes) cannon azimuth,
+// elevation and fire.
+struct ArmOutputs {
+    float throttle, outer, inner, az, el, fire;
+};
+
+// onboard_features.cuh:88-513 with the LiDAR passes replaced by `scan`, on
+// the four lanes of a quad: lane a evaluates arm a's terms (the two per-arm
+// loops, :114-125 and :376-391, hold most of the controller's transcendental
+// calls) and the four lanes repeat the shared chain.  The arm sums and the
+// running maximum are formed in the reference's order from quad broadcasts,
+// so every value is the one the per-environment loop forms.
+__device__ ArmOutputs prior_features(const float *input_obs, const float *input_mission,
+                                     const ScanResult &scan, int a) {
     const float pi = kPi;
     const float max_installed = 294.2f * 0.85f;
     const float idle_frac = 0.08f;
@@ -473,18 +491,21 @@ __device__ void prior_features(const float *input_obs, const float *input_missio
     const float ox = o[10], oy = o[11], oz = o[12];
     const float omega_norm = ob_norm3(ox, oy, oz);
 
-    float spool[4], thrust[4], outer[4], ft[4], fz[4];
+    // Arm a of the four (this lane's); the quad exchanges the arm forces.
+    const float spool = ob_clamp(ob_obs(input_obs[16 + a]), 0.0f, 1.0f);
+    const float thrust = max_installed * (idle_frac + (1.0f - idle_frac) * spool);
+    const float outer = atan2f(ob_obs(input_obs[20 + a]), ob_obs(input_obs[24 + a]));
+    const SinCos o_sc = sin_cos(outer);
+    const float c_inner = cosf(ob_obs(input_obs[28 + a]));
+    const float fz_a = thrust * o_sc.c * c_inner;
+    const float ft_a = thrust * o_sc.s * c_inner;
+    const float fz[4] = {quad_lane<0>(fz_a), quad_lane<1>(fz_a), quad_lane<2>(fz_a),
+                         quad_lane<3>(fz_a)};
+    const float ft[4] = {quad_lane<0>(ft_a), quad_lane<1>(ft_a), quad_lane<2>(ft_a),
+                         quad_lane<3>(ft_a)};
     float total_fz = 0.0f, jammed_yaw_ft = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        spool[i] = ob_clamp(o[16 + i], 0.0f, 1.0f);
-        thrust[i] = max_installed * (idle_frac + (1.0f - idle_frac) * spool[i]);
-        outer[i] = atan2f(o[20 + i], o[24 + i]);
-        const float inner = o[28 + i];
-        const SinCos o_sc = sin_cos(outer[i]);
-        const float c_inner = cosf(inner);
-        fz[i] = thrust[i] * o_sc.c * c_inner;
-        ft[i] = thrust[i] * o_sc.s * c_inner;
         total_fz += fz[i];
         jammed_yaw_ft += ft[i];
     }
@@ -687,52 +708,50 @@ __device__ void prior_features(const float *input_obs, const float *input_missio
     const float tau_y_cmd = ob_clamp(95.0f * e_ry - 64.0f * oy - 0.90f * tau_y_net - tau_y_par,
                                      -max_txy, max_txy);
     const float tau_z_cmd = ob_clamp(22.0f * yaw_err - 18.0f * oz, -70.0f, 70.0f);
-    const float fz_cmd[4] = {0.25f * fz_des - tau_y_cmd * 0.5f, 0.25f * fz_des + tau_x_cmd * 0.5f,
-                             0.25f * fz_des + tau_y_cmd * 0.5f, 0.25f * fz_des - tau_x_cmd * 0.5f};
+    // {q - ty, q + tx, q + ty, q - tx}[a]; q - t and q + (-t) are the same
+    // IEEE operation.
+    const float half_tx = tau_x_cmd * 0.5f, half_ty = tau_y_cmd * 0.5f;
+    const float fz_cmd =
+        0.25f * fz_des + (a == 0 ? -half_ty : (a == 1 ? half_tx : (a == 2 ? half_ty : -half_tx)));
     const float yaw_ft = (tau_z_cmd - 0.40f * jammed_yaw_ft) * 0.25f;
-    float outer_cmd[4], inner_cmd[4], throttle[4], u_raw[4];
+    float outer_cmd, inner_cmd, throttle;
     const float fx_outer = ft[3] - ft[1];
     const float fy_outer = ft[0] - ft[2];
     const float fx_rem = fx_body - fx_outer, fy_rem = fy_body - fy_outer;
     const float max_sin_inner =
         lateral ? 0.44f : (active_slalom ? 0.42f : (heavy_cargo ? 0.22f : 0.32f));
     const float spool_gain = turbine_out ? 10.5f : (heavy_cargo ? 4.5f : 2.4f);
-    float max_raw = -__builtin_huge_valf();
     const bool land_idle = landing && pz <= 0.638f && up_horiz < 0.85f && fabsf(vz) < 0.20f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float yaw_alpha = asinf(ob_clamp(yaw_ft / fmaxf(thrust[i], 30.0f), -0.35f, 0.35f));
-        outer_cmd[i] = ob_clamp(6.5f * ob_wrap(yaw_alpha, outer[i]), -outer_limit, outer_limit);
-        const float urx = i == 0 ? 1.0f : (i == 2 ? -1.0f : 0.0f);
-        const float ury = i == 1 ? 1.0f : (i == 3 ? -1.0f : 0.0f);
-        const float fr_req = 0.5f * (fx_rem * urx + fy_rem * ury);
-        const float sin_in =
-            ob_clamp(fr_req / fmaxf(thrust[i], 40.0f), -max_sin_inner, max_sin_inner);
-        inner_cmd[i] = ob_clamp(asinf(sin_in), -inner_limit * 0.90f, inner_limit * 0.90f);
-        const float nominal_cos = fmaxf(cosf(yaw_alpha) * cosf(inner_cmd[i]), 0.70f);
-        float target_thrust = fmaxf(fz_cmd[i], 0.0f) / nominal_cos;
-        if (land_idle) target_thrust = 0.15f * weight * 0.25f;
-        const float u_des =
-            ob_clamp((target_thrust - min_thrust) / (max_installed - min_thrust), 0.0f, 1.0f);
-        u_raw[i] = u_des + spool_gain * (u_des - spool[i]);
-        max_raw = fmaxf(max_raw, u_raw[i]);
-    }
+    const float yaw_alpha = asinf(ob_clamp(yaw_ft / fmaxf(thrust, 30.0f), -0.35f, 0.35f));
+    outer_cmd = ob_clamp(6.5f * ob_wrap(yaw_alpha, outer), -outer_limit, outer_limit);
+    const float urx = a == 0 ? 1.0f : (a == 2 ? -1.0f : 0.0f);
+    const float ury = a == 1 ? 1.0f : (a == 3 ? -1.0f : 0.0f);
+    const float fr_req = 0.5f * (fx_rem * urx + fy_rem * ury);
+    const float sin_in = ob_clamp(fr_req / fmaxf(thrust, 40.0f), -max_sin_inner, max_sin_inner);
+    inner_cmd = ob_clamp(asinf(sin_in), -inner_limit * 0.90f, inner_limit * 0.90f);
+    const float nominal_cos = fmaxf(cosf(yaw_alpha) * cosf(inner_cmd), 0.70f);
+    float target_thrust = fmaxf(fz_cmd, 0.0f) / nominal_cos;
+    if (land_idle) target_thrust = 0.15f * weight * 0.25f;
+    const float u_des =
+        ob_clamp((target_thrust - min_thrust) / (max_installed - min_thrust), 0.0f, 1.0f);
+    const float u_raw = u_des + spool_gain * (u_des - spool);
+    // The reference's running maximum over arms 0..3, from -inf.
+    float max_raw = -__builtin_huge_valf();
+    max_raw = fmaxf(max_raw, quad_lane<0>(u_raw));
+    max_raw = fmaxf(max_raw, quad_lane<1>(u_raw));
+    max_raw = fmaxf(max_raw, quad_lane<2>(u_raw));
+    max_raw = fmaxf(max_raw, quad_lane<3>(u_raw));
     const float excess = ob_clamp(max_raw - 1.0f, 0.0f, urgent_climb ? 0.10f : 0.45f);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        throttle[i] = ob_clamp(u_raw[i] - (need_headroom ? excess : 0.0f), 0.0f, 1.0f);
+    throttle = ob_clamp(u_raw - (need_headroom ? excess : 0.0f), 0.0f, 1.0f);
     const bool inv_mode = ct < 0.20f;
     if (inv_mode) {
         const float inv_rx = te_norm > 1.0e-5f ? e_rx : tilt;
         const float tx_inv = 130.0f * inv_rx - 52.0f * ox;
         const float ty_inv = 130.0f * e_ry - 52.0f * oy;
-        const float arm_mom[4] = {-ty_inv, tx_inv, ty_inv, -tx_inv};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            throttle[i] = arm_mom[i] > 12.0f ? 0.58f : 0.0f;
-            outer_cmd[i] = ob_clamp(-outer[i] * 6.0f, -outer_limit, outer_limit);
-            inner_cmd[i] = 0.0f;
-        }
+        const float arm_mom = a == 0 ? -ty_inv : (a == 1 ? tx_inv : (a == 2 ? ty_inv : -tx_inv));
+        throttle = arm_mom > 12.0f ? 0.58f : 0.0f;
+        outer_cmd = ob_clamp(-outer * 6.0f, -outer_limit, outer_limit);
+        inner_cmd = 0.0f;
     }
 
     const float to_x = tx - px, to_y = ty - py, to_z = tz - pz;
@@ -793,8 +812,7 @@ __device__ void prior_features(const float *input_obs, const float *input_missio
             ob_clamp(0.90f * (desired_roll - roll_right) - 0.34f * ox, -0.45f, 0.45f);
         const float u0 = ob_clamp(u_coll + diff_u, 0.05f, 1.0f);
         const float u1 = ob_clamp(u_coll - diff_u, 0.05f, 1.0f);
-        throttle[0] = throttle[2] = u0;
-        throttle[1] = throttle[3] = u1;
+        throttle = (a & 1) ? u1 : u0;
         const float pitch_up = asinf(ob_clamp(r20, -1.0f, 1.0f));
         const float climb_des = ob_clamp(0.42f * gz, -5.0f, 5.0f);
         const float climb_err = climb_des - vz;
@@ -812,11 +830,10 @@ __device__ void prior_features(const float *input_obs, const float *input_missio
         const float q_up = cos_bank * theta_dot - sin_bank * psi_dot;
         const float r_left = sin_bank * theta_dot + cos_bank * psi_dot;
         const float gimbal = pi / 6.0f;
-        inner_cmd[0] = ob_clamp(0.85f * (q_up + oy) + 0.03f, -gimbal, gimbal);
-        inner_cmd[1] = ob_clamp(-0.65f * (r_left - oz) - 0.025f * vb_y, -gimbal, gimbal);
-        inner_cmd[2] = inner_cmd[3] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) outer_cmd[i] = 0.0f;
+        const float inner0 = ob_clamp(0.85f * (q_up + oy) + 0.03f, -gimbal, gimbal);
+        const float inner1 = ob_clamp(-0.65f * (r_left - oz) - 0.025f * vb_y, -gimbal, gimbal);
+        inner_cmd = a == 0 ? inner0 : (a == 1 ? inner1 : 0.0f);
+        outer_cmd = 0.0f;
         const float oppx = brx - vx * 0.10f, oppy = bry - vy * 0.10f, oppz = brz - vz * 0.10f;
         const float bdist = fmaxf(ob_norm3(oppx, oppy, oppz), 1.0f);
         const bool head_on = bwb_arena && btx * px + bty * py < -800.0f && bdist > 45.0f;
@@ -838,15 +855,14 @@ __device__ void prior_features(const float *input_obs, const float *input_missio
         norm_el = arena ? ob_clamp(b_el / cannon_el_lim, -1.0f, 1.0f) : 0.0f;
         norm_fire = b_fire ? 0.8f : -0.8f;
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        n[i] = ob_clamp(throttle[i] * 2.0f - 1.0f, -1.0f, 1.0f);
-        n[4 + i] = ob_clamp(outer_cmd[i] / outer_limit, -1.0f, 1.0f);
-        n[8 + i] = ob_clamp(inner_cmd[i] / inner_limit, -1.0f, 1.0f);
-    }
-    n[12] = norm_az;
-    n[13] = norm_el;
-    n[14] = norm_fire;
+    ArmOutputs out;
+    out.throttle = ob_clamp(throttle * 2.0f - 1.0f, -1.0f, 1.0f);
+    out.outer = ob_clamp(outer_cmd / outer_limit, -1.0f, 1.0f);
+    out.inner = ob_clamp(inner_cmd / inner_limit, -1.0f, 1.0f);
+    out.az = norm_az;
+    out.el = norm_el;
+    out.fire = norm_fire;
+    return out;
 }
 
 struct OnboardRows {
@@ -972,18 +988,20 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
 }
 
 // Phase 2: the tactical features and the controller, from the parked scan
-// result.  They are independent, so a 128-thread block runs them on two
-// waves for the same 64 environments (lane = environment): wave 0 the
-// tactical features, wave 1 the controller.  Each is a long scalar chain
-// (tens of transcendental calls) and only a few waves exist per launch, so
-// splitting the chain shortens the launch and spreads it over twice the
-// SIMDs.  Values are formed in registers and then stored to each
+// result.  A 320-thread workgroup covers 64 environments: wave 0 runs the
+// tactical features, one lane per environment; waves 1..4 run the
+// controller, one quad of lanes per environment (16 per wave), lane a of the
+// quad on arm a.  Both are long scalar chains and few waves exist per
+// launch, so splitting the work shortens the chains and spreads them over
+// more SIMDs.  Values are formed in registers and then stored to each
 // destination (the tactical / prior rows and, for the actor, their copies in
 // proprio and mission_vec).
 __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(OnboardRows rows) {
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    for (size_t env = (size_t)blockIdx.x * 64 + lane; env < rows.batch;
+    const int slot = w == 0 ? lane : 16 * (w - 1) + (lane >> 2);  // environment within the 64
+    const int a = lane & 3;
+    for (size_t env = (size_t)blockIdx.x * 64 + slot; env < rows.batch;
          env += (size_t)gridDim.x * 64) {
         const float *obs = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
         const float *mission =
@@ -1013,19 +1031,35 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
         s.cluster_y_sum = prior[4];
         s.min_ray = __float_as_int(prior[5]);
         s.cluster_count = __float_as_int(prior[6]);
-        float n[15];
-        prior_features(obs, mission, s, n);
-#pragma unroll
-        for (int i = 0; i < 15; ++i) prior[i] = n[i];
+        const ArmOutputs n = prior_features(obs, mission, s, a);
+        // The parked result was read by all four lanes before the chain;
+        // each lane now writes its arm's three values, lane 0 the cannon's.
+        prior[a] = n.throttle;
+        prior[4 + a] = n.outer;
+        prior[8 + a] = n.inner;
+        if (a == 0) {
+            prior[12] = n.az;
+            prior[13] = n.el;
+            prior[14] = n.fire;
+        }
         if (rows.proprio) {
-            float *p = rows.proprio + env * 91, *mv = rows.mission_vec + env * 49;
-#pragma unroll
-            for (int i = 0; i < 15; ++i) {
-                p[76 + i] = n[i];
-                mv[34 + i] = n[i];
+            float *p = rows.proprio + env * 91 + 76, *mv = rows.mission_vec + env * 49 + 34;
+            p[a] = n.throttle;
+            p[4 + a] = n.outer;
+            p[8 + a] = n.inner;
+            mv[a] = n.throttle;
+            mv[4 + a] = n.outer;
+            mv[8 + a] = n.inner;
+            if (a == 0) {
+                p[12] = n.az;
+                p[13] = n.el;
+                p[14] = n.fire;
+                mv[12] = n.az;
+                mv[13] = n.el;
+                mv[14] = n.fire;
             }
         }
-        if (rows.diag) {
+        if (rows.diag && a == 0) {
             float *d = rows.diag + env * 4;
             d[0] = s.min_r;
             d[1] = (float)s.min_ray;
