@@ -452,6 +452,19 @@ __device__ __forceinline__ float quad_lane(float v) {
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), K * 0x55, 0xF, 0xF, false));
 }
 
+// The four lanes' values of v, in every lane of the quad.
+struct Quad4 {
+    float v[4];
+};
+__device__ __forceinline__ Quad4 quad_all(float v) {
+    return Quad4{{quad_lane<0>(v), quad_lane<1>(v), quad_lane<2>(v), quad_lane<3>(v)}};
+}
+
+// Quad lane a's choice among four values.
+__device__ __forceinline__ float quad_pick(int a, float v0, float v1, float v2, float v3) {
+    return a == 0 ? v0 : (a == 1 ? v1 : (a == 2 ? v2 : v3));
+}
+
 // One lane's share of the prior features: its arm's throttle, outer and
 // inner commands, and (identical in the four lanes) cannon azimuth,
 // elevation and fire.
@@ -461,10 +474,13 @@ struct ArmOutputs {
 
 // onboard_features.cuh:88-513 with the LiDAR passes replaced by `scan`, on
 // the four lanes of a quad: lane a evaluates arm a's terms (the two per-arm
-// loops, :114-125 and :376-391, hold most of the controller's transcendental
-// calls) and the four lanes repeat the shared chain.  The arm sums and the
-// running maximum are formed in the reference's order from quad broadcasts,
-// so every value is the one the per-environment loop forms.
+// loops, :114-125 and :376-391) and the four lanes repeat the shared chain,
+// except that independent calls of one function are spread over the quad
+// (four atan2, four atanh, four sine/cosine pairs, four angle wraps) and
+// their results broadcast.  The arm sums and the running maximum are formed
+// in the reference's order from quad broadcasts, so every value is the one
+// the per-environment code forms.  The statements are reordered only where
+// a value is needed earlier for such a group.
 __device__ ArmOutputs prior_features(const float *input_obs, const float *input_mission,
                                      const ScanResult &scan, int a) {
     const float pi = kPi;
@@ -485,6 +501,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     const float px = o[0], py = o[1], pz = o[2], vx = o[3], vy = o[4], vz = o[5];
     const Attitude att = attitude_of(o[6], o[7], o[8], o[9]);
     const float qw = att.qw, qx = att.qx, qy = att.qy, qz = att.qz;
+    const float ux = -qx, uy = -qy, uz = -qz;
     const float r00 = att.r[0], r01 = att.r[1], r02 = att.r[2];
     const float r10 = att.r[3], r11 = att.r[4], r12 = att.r[5];
     const float r20 = att.r[6], r21 = att.r[7], r22 = att.r[8];
@@ -499,15 +516,12 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     const float c_inner = cosf(ob_obs(input_obs[28 + a]));
     const float fz_a = thrust * o_sc.c * c_inner;
     const float ft_a = thrust * o_sc.s * c_inner;
-    const float fz[4] = {quad_lane<0>(fz_a), quad_lane<1>(fz_a), quad_lane<2>(fz_a),
-                         quad_lane<3>(fz_a)};
-    const float ft[4] = {quad_lane<0>(ft_a), quad_lane<1>(ft_a), quad_lane<2>(ft_a),
-                         quad_lane<3>(ft_a)};
+    const Quad4 fz = quad_all(fz_a), ft = quad_all(ft_a);
     float total_fz = 0.0f, jammed_yaw_ft = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        total_fz += fz[i];
-        jammed_yaw_ft += ft[i];
+        total_fz += fz.v[i];
+        jammed_yaw_ft += ft.v[i];
     }
     const bool landing = m[1] > 0.75f;
     const bool cargo = m[2] > 0.75f;
@@ -517,6 +531,11 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     const bool slalom = m[4] > 0.75f && !lateral;
     const bool dodge = m[5] > 0.75f;
     const bool arena = m[6] > 0.75f;
+    const bool bwb_arena = m[6] > 0.75f && m[4] < -0.25f;
+    const bool bwb_cruise = m[4] > 0.75f && m[2] > 0.25f;
+    const bool bwb_intercept = m[6] > 0.75f && m[5] > 0.60f;
+    const bool bwb_endurance = bwb_cruise && m[0] > 0.25f;
+    const bool bwb = bwb_arena || bwb_cruise || bwb_intercept;
     const float fuel = ob_clamp(o[40], 0.0f, 1.0f) * 9.0f;
     const float ammo_mass = ob_clamp(o[47], 0.0f, 4.0f) * 6.0f;
     const bool payload = o[41] > 0.5f;
@@ -525,16 +544,26 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     const float body_z_x = 2.0f * (qx * qz + qw * qy);
     const float body_z_y = 2.0f * (qy * qz - qw * qx);
     const float ct = ob_clamp(r22, -1.0f, 1.0f);
-    const float yaw = atan2f(r10, r00);
-    const float tau_x_actual = fz[1] - fz[3];
-    const float tau_y_actual = fz[2] - fz[0];
+    const float tau_x_actual = fz.v[1] - fz.v[3];
+    const float tau_y_actual = fz.v[2] - fz.v[0];
     const float az_actual = (total_fz * ct - weight) / mass;
     const bool heavy_cargo = cargo && payload;
     const bool landing_like = landing || heavy_cargo;
 
-    const float relx = atanhf(ob_clamp(m[7], -0.9995f, 0.9995f)) * 20.0f;
-    const float rely = atanhf(ob_clamp(m[8], -0.9995f, 0.9995f)) * 20.0f;
-    const float relz = atanhf(ob_clamp(m[9], -0.9995f, 0.9995f)) * 20.0f;
+    // Independent calls of one function, one per lane of the quad: yaw, the
+    // opponent bearing, the BWB roll and ground-track angles; the mission
+    // offsets (atanh at the standard clamp, and the first at the BWB clamp).
+    const Quad4 angles = quad_all(atan2f(quad_pick(a, r10, m[1], r21, vy),
+                                         quad_pick(a, r00, m[2], r22, vx)));
+    const float yaw = angles.v[0], opp_bearing = angles.v[1];
+    const float roll_right = angles.v[2], track_yaw = angles.v[3];
+    const Quad4 offsets = quad_all(atanhf(quad_pick(
+        a, ob_clamp(m[7], -0.9995f, 0.9995f), ob_clamp(m[8], -0.9995f, 0.9995f),
+        ob_clamp(m[9], -0.9995f, 0.9995f), ob_clamp(m[7], -0.9999f, 0.9999f))));
+
+    const float relx = offsets.v[0] * 20.0f;
+    const float rely = offsets.v[1] * 20.0f;
+    const float relz = offsets.v[2] * 20.0f;
     float tx = (arena || lateral) ? px + relx : 0.0f;
     if (cargo) tx = 15.0f;
     if (slalom) tx = 36.0f;
@@ -563,12 +592,39 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     const float errx = ex - px, erry = ey - py;
     const float horiz_dist = hypotf(errx, erry);
 
+    // Cannon aim point in the body frame (formed here so that its two
+    // angles join the quad's next atan2 round).
+    const float to_x = tx - px, to_y = ty - py, to_z = tz - pz;
+    const float dist = fmaxf(ob_norm3(to_x, to_y, to_z), 1.0f);
+    const float flight = dist / 20.0f;
+    const float aim_x = to_x - vx * (0.65f * flight);
+    const float aim_y = to_y - vy * (0.65f * flight);
+    const float aim_z = to_z - vz * (0.65f * flight) + 0.53f * gravity * flight * flight;
+    const float cx = uy * aim_z - uz * aim_y + qw * aim_x;
+    const float cyq = uz * aim_x - ux * aim_z + qw * aim_y;
+    const float cz = ux * aim_y - uy * aim_x + qw * aim_z;
+    const float aim_bx = aim_x + 2.0f * (uy * cz - uz * cyq);
+    const float aim_by = aim_y + 2.0f * (uz * cx - ux * cz);
+    const float aim_bz = aim_z + 2.0f * (ux * cyq - uy * cx);
+    const Quad4 bearings = quad_all(atan2f(
+        quad_pick(a, ty - py, scan.min_r_dy, aim_by, aim_bz),
+        quad_pick(a, tx - px, scan.min_r_dx, aim_bx, fmaxf(hypotf(aim_bx, aim_by), 0.2f))));
+    const float raw_bearing = bearings.v[0], min_az = bearings.v[1];
+    const float des_cannon_az =
+        ob_clamp(bearings.v[2], cannon_az_ctr - cannon_az_half, cannon_az_ctr + cannon_az_half);
+    const float des_cannon_el = ob_clamp(bearings.v[3], -cannon_el_lim, cannon_el_lim);
+
+    // Sine and cosine of yaw, of the closest return's bearing, of the BWB
+    // roll, and of the slalom hill phase.
+    const float hill = ob_clamp((px - 6.0f) / 30.0f, 0.0f, 1.0f);
+    const SinCos sc = sin_cos(quad_pick(a, yaw, min_az, roll_right, pi * hill));
+    const Quad4 sines = quad_all(sc.s), cosines = quad_all(sc.c);
+    const float cyaw = cosines.v[0], syaw = sines.v[0];
+
     float avoid_x = 0.0f, avoid_y = 0.0f, slalom_speed = 3.8f, nearest_dx = 30.0f;
     if (dodge && scan.min_r < 7.5f) {
-        const float min_az = atan2f(scan.min_r_dy, scan.min_r_dx);
-        const SinCos az = sin_cos(min_az);
-        avoid_x = -az.s * 2.2f;
-        avoid_y = az.c * 2.2f;
+        avoid_x = -sines.v[1] * 2.2f;
+        avoid_y = cosines.v[1] * 2.2f;
     }
     const float min_dx_c = scan.min_dx_c;
     const int cluster_count = scan.cluster_count;
@@ -584,10 +640,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     if (lane_err > 1.05f) speed_limit = 1.55f;
     if (min_dx_c >= 6.6f && px > 4.0f) speed_limit = 3.10f;
     if (has_slalom_obs) slalom_speed = speed_limit;
-    if (slalom && horiz_dist > 3.5f) {
-        const float hill = ob_clamp((px - 6.0f) / 30.0f, 0.0f, 1.0f);
-        ez = 2.5f * sinf(pi * hill) + 8.0f;
-    }
+    if (slalom && horiz_dist > 3.5f) ez = 2.5f * sines.v[3] + 8.0f;
     const float upx = ex - px, upy = ey - py, upz = ez - pz;
     const float up_horiz = hypotf(upx, upy);
     const bool active_slalom = slalom && nearest_dx < 10.2f && horiz_dist > 3.0f;
@@ -669,15 +722,12 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
         (mass * des_ax + damp_v * vx - tilt_comp * total_fz * body_z_x) * horiz_scale;
     const float fy_world =
         (mass * des_ay + damp_v * vy - tilt_comp * total_fz * body_z_y) * horiz_scale;
-    const SinCos yaw_sc = sin_cos(yaw);
-    const float cyaw = yaw_sc.c, syaw = yaw_sc.s;
     const float max_fh =
         active_slalom ? 105.0f : (lateral ? 125.0f : (heavy_cargo ? 52.0f : 80.0f));
     const float fx_body = ob_clamp(cyaw * fx_world + syaw * fy_world, -max_fh, max_fh);
     const float fy_body = ob_clamp(-syaw * fx_world + cyaw * fy_world, -max_fh, max_fh);
 
     const float cw_x = body_z_y, cw_y = -body_z_x;
-    const float ux = -qx, uy = -qy, uz = -qz;
     const float tt_x = 2.0f * (-uz * cw_y), tt_y = 2.0f * (uz * cw_x);
     const float tt_z = 2.0f * (ux * cw_y - uy * cw_x);
     const float te_x = cw_x + qw * tt_x + (uy * tt_z - uz * tt_y);
@@ -689,13 +739,64 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
 
     const bool inv_hold_yaw = (inversion || arena) && (pz < 6.0f || vz < -0.5f || ct < 0.88f);
     const bool opp_bearing_valid = arena && fabsf(m[1]) + fabsf(m[2]) > 0.1f;
-    const float opp_bearing = atan2f(m[1], m[2]);
-    const float raw_bearing = atan2f(ty - py, tx - px);
     const float target_bearing = opp_bearing_valid ? opp_bearing : raw_bearing;
     const float desired_yaw = arena && horiz_dist > 1.0f && !inv_hold_yaw
                                   ? target_bearing - cannon_az_ctr
                                   : (inv_hold_yaw ? yaw : 0.0f);
-    const float yaw_err = ob_wrap(desired_yaw, yaw);
+
+    // BWB geometry (onboard_features.cuh:437-510), up to the angles its two
+    // wraps need; the control law follows after the shared part.
+    float vb_x = 0.0f, vb_y = 0.0f, brx = 0.0f, bry = 0.0f, btx = 0.0f, bty = 0.0f, gz = 0.0f;
+    float gdist = 0.0f, gamma_des = 0.0f, bdist = 0.0f, bbx = 0.0f;
+    float desired_yaw_b = 0.0f, course_yaw = 0.0f, b_az = 0.0f, b_el = 0.0f;
+    if (bwb) {
+        vb_x = r00 * vx + r10 * vy + r20 * vz;
+        vb_y = r01 * vx + r11 * vy + r21 * vz;
+        brx = offsets.v[3] * 20.0f;
+        const Quad4 b_offsets = quad_all(atanhf(quad_pick(a, ob_clamp(m[8], -0.9999f, 0.9999f),
+                                                          ob_clamp(m[9], -0.9999f, 0.9999f),
+                                                          0.0f, 0.0f)));
+        bry = b_offsets.v[0] * 20.0f;
+        const float brz = b_offsets.v[1] * 20.0f;
+        btx = px + brx;
+        bty = py + bry;
+        float btz = pz + brz;
+        const float rxy = hypotf(px, py);
+        const float pull_b = ob_clamp((rxy - 235.0f) / 45.0f, 0.0f, 0.85f);
+        if (arena && rxy > 235.0f) { btx *= 1.0f - pull_b; bty *= 1.0f - pull_b; }
+        if (arena) btz = ob_clamp(btz, 28.0f, 135.0f);
+        const float gx = btx - px, gy = bty - py;
+        gz = btz - pz;
+        gdist = fmaxf(ob_norm3(gx, gy, gz), 1.0f);
+        const float gs = hypotf(vx, vy);
+        course_yaw = gs > 2.5f ? track_yaw : yaw;
+        const float climb_des = ob_clamp(0.42f * gz, -5.0f, 5.0f);
+        const float oppx = brx - vx * 0.10f, oppy = bry - vy * 0.10f, oppz = brz - vz * 0.10f;
+        bdist = fmaxf(ob_norm3(oppx, oppy, oppz), 1.0f);
+        const bool head_on = bwb_arena && btx * px + bty * py < -800.0f && bdist > 45.0f;
+        const float closing = head_on ? 75.0f + 2.0f * fmaxf(vb_x, 0.0f) : 75.0f;
+        const float bflight = bdist / closing;
+        const float bax = oppx, bay = oppy;
+        const float baz =
+            oppz + (head_on ? -vz * (0.85f * bflight) : 0.0f) + 0.50f * gravity * bflight * bflight;
+        bbx = r00 * bax + r10 * bay + r20 * baz;
+        const float bby = r01 * bax + r11 * bay + r21 * baz;
+        const float bbz = r02 * bax + r12 * bay + r22 * baz;
+        const Quad4 b_angles = quad_all(atan2f(
+            quad_pick(a, gy, climb_des, bby, bbz),
+            quad_pick(a, gx, fmaxf(gs, 14.0f), fmaxf(bbx, 0.2f), fmaxf(hypotf(bbx, bby), 0.2f))));
+        desired_yaw_b = b_angles.v[0];
+        gamma_des = b_angles.v[1];
+        b_az = ob_clamp(b_angles.v[2], -pi / 6.0f, pi / 6.0f);
+        b_el = ob_clamp(b_angles.v[3], -cannon_el_lim, cannon_el_lim);
+    }
+
+    // The four angle wraps, one per lane: yaw error, cannon azimuth error,
+    // BWB course error, BWB cannon azimuth error.
+    const Quad4 wraps = quad_all(ob_wrap(quad_pick(a, desired_yaw, des_cannon_az, desired_yaw_b,
+                                                   b_az),
+                                         quad_pick(a, yaw, o[44], course_yaw, o[44])));
+    const float yaw_err = wraps.v[0];
 
     const float parasite_scale = turbine_out ? 0.35f : 1.0f;
     const float tau_x_par = -0.1625f * fy_body * parasite_scale;
@@ -711,12 +812,11 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     // {q - ty, q + tx, q + ty, q - tx}[a]; q - t and q + (-t) are the same
     // IEEE operation.
     const float half_tx = tau_x_cmd * 0.5f, half_ty = tau_y_cmd * 0.5f;
-    const float fz_cmd =
-        0.25f * fz_des + (a == 0 ? -half_ty : (a == 1 ? half_tx : (a == 2 ? half_ty : -half_tx)));
+    const float fz_cmd = 0.25f * fz_des + quad_pick(a, -half_ty, half_tx, half_ty, -half_tx);
     const float yaw_ft = (tau_z_cmd - 0.40f * jammed_yaw_ft) * 0.25f;
     float outer_cmd, inner_cmd, throttle;
-    const float fx_outer = ft[3] - ft[1];
-    const float fy_outer = ft[0] - ft[2];
+    const float fx_outer = ft.v[3] - ft.v[1];
+    const float fy_outer = ft.v[0] - ft.v[2];
     const float fx_rem = fx_body - fx_outer, fy_rem = fy_body - fy_outer;
     const float max_sin_inner =
         lateral ? 0.44f : (active_slalom ? 0.42f : (heavy_cargo ? 0.22f : 0.32f));
@@ -724,8 +824,8 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     const bool land_idle = landing && pz <= 0.638f && up_horiz < 0.85f && fabsf(vz) < 0.20f;
     const float yaw_alpha = asinf(ob_clamp(yaw_ft / fmaxf(thrust, 30.0f), -0.35f, 0.35f));
     outer_cmd = ob_clamp(6.5f * ob_wrap(yaw_alpha, outer), -outer_limit, outer_limit);
-    const float urx = a == 0 ? 1.0f : (a == 2 ? -1.0f : 0.0f);
-    const float ury = a == 1 ? 1.0f : (a == 3 ? -1.0f : 0.0f);
+    const float urx = quad_pick(a, 1.0f, 0.0f, -1.0f, 0.0f);
+    const float ury = quad_pick(a, 0.0f, 1.0f, 0.0f, -1.0f);
     const float fr_req = 0.5f * (fx_rem * urx + fy_rem * ury);
     const float sin_in = ob_clamp(fr_req / fmaxf(thrust, 40.0f), -max_sin_inner, max_sin_inner);
     inner_cmd = ob_clamp(asinf(sin_in), -inner_limit * 0.90f, inner_limit * 0.90f);
@@ -736,11 +836,10 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
         ob_clamp((target_thrust - min_thrust) / (max_installed - min_thrust), 0.0f, 1.0f);
     const float u_raw = u_des + spool_gain * (u_des - spool);
     // The reference's running maximum over arms 0..3, from -inf.
+    const Quad4 u_all = quad_all(u_raw);
     float max_raw = -__builtin_huge_valf();
-    max_raw = fmaxf(max_raw, quad_lane<0>(u_raw));
-    max_raw = fmaxf(max_raw, quad_lane<1>(u_raw));
-    max_raw = fmaxf(max_raw, quad_lane<2>(u_raw));
-    max_raw = fmaxf(max_raw, quad_lane<3>(u_raw));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) max_raw = fmaxf(max_raw, u_all.v[i]);
     const float excess = ob_clamp(max_raw - 1.0f, 0.0f, urgent_climb ? 0.10f : 0.45f);
     throttle = ob_clamp(u_raw - (need_headroom ? excess : 0.0f), 0.0f, 1.0f);
     const bool inv_mode = ct < 0.20f;
@@ -748,29 +847,13 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
         const float inv_rx = te_norm > 1.0e-5f ? e_rx : tilt;
         const float tx_inv = 130.0f * inv_rx - 52.0f * ox;
         const float ty_inv = 130.0f * e_ry - 52.0f * oy;
-        const float arm_mom = a == 0 ? -ty_inv : (a == 1 ? tx_inv : (a == 2 ? ty_inv : -tx_inv));
+        const float arm_mom = quad_pick(a, -ty_inv, tx_inv, ty_inv, -tx_inv);
         throttle = arm_mom > 12.0f ? 0.58f : 0.0f;
         outer_cmd = ob_clamp(-outer * 6.0f, -outer_limit, outer_limit);
         inner_cmd = 0.0f;
     }
 
-    const float to_x = tx - px, to_y = ty - py, to_z = tz - pz;
-    const float dist = fmaxf(ob_norm3(to_x, to_y, to_z), 1.0f);
-    const float flight = dist / 20.0f;
-    const float aim_x = to_x - vx * (0.65f * flight);
-    const float aim_y = to_y - vy * (0.65f * flight);
-    const float aim_z = to_z - vz * (0.65f * flight) + 0.53f * gravity * flight * flight;
-    const float cx = uy * aim_z - uz * aim_y + qw * aim_x;
-    const float cyq = uz * aim_x - ux * aim_z + qw * aim_y;
-    const float cz = ux * aim_y - uy * aim_x + qw * aim_z;
-    const float aim_bx = aim_x + 2.0f * (uy * cz - uz * cyq);
-    const float aim_by = aim_y + 2.0f * (uz * cx - ux * cz);
-    const float aim_bz = aim_z + 2.0f * (ux * cyq - uy * cx);
-    const float des_cannon_az = ob_clamp(atan2f(aim_by, aim_bx), cannon_az_ctr - cannon_az_half,
-                                         cannon_az_ctr + cannon_az_half);
-    const float des_cannon_el = ob_clamp(atan2f(aim_bz, fmaxf(hypotf(aim_bx, aim_by), 0.2f)),
-                                         -cannon_el_lim, cannon_el_lim);
-    const float aim_err = hypotf(ob_wrap(des_cannon_az, o[44]), des_cannon_el - o[45]);
+    const float aim_err = hypotf(wraps.v[1], des_cannon_el - o[45]);
     const bool fire = arena && !inv_mode && o[46] <= 0.02f && o[47] > 0.01f && aim_err < 0.28f &&
                       dist < 34.0f;
     const bool cannon = arena && !inv_mode;
@@ -780,33 +863,13 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     float norm_el = cannon ? ob_clamp(des_cannon_el / cannon_el_lim, -1.0f, 1.0f) : 0.0f;
     float norm_fire = fire ? 0.8f : -0.8f;
 
-    const bool bwb_arena = m[6] > 0.75f && m[4] < -0.25f;
-    const bool bwb_cruise = m[4] > 0.75f && m[2] > 0.25f;
-    const bool bwb_intercept = m[6] > 0.75f && m[5] > 0.60f;
-    const bool bwb_endurance = bwb_cruise && m[0] > 0.25f;
-    if (bwb_arena || bwb_cruise || bwb_intercept) {
-        const float vb_x = r00 * vx + r10 * vy + r20 * vz;
-        const float vb_y = r01 * vx + r11 * vy + r21 * vz;
-        const float brx = atanhf(ob_clamp(m[7], -0.9999f, 0.9999f)) * 20.0f;
-        const float bry = atanhf(ob_clamp(m[8], -0.9999f, 0.9999f)) * 20.0f;
-        const float brz = atanhf(ob_clamp(m[9], -0.9999f, 0.9999f)) * 20.0f;
-        float btx = px + brx, bty = py + bry, btz = pz + brz;
-        const float rxy = hypotf(px, py);
-        const float pull_b = ob_clamp((rxy - 235.0f) / 45.0f, 0.0f, 0.85f);
-        if (arena && rxy > 235.0f) { btx *= 1.0f - pull_b; bty *= 1.0f - pull_b; }
-        if (arena) btz = ob_clamp(btz, 28.0f, 135.0f);
-        const float gx = btx - px, gy = bty - py, gz = btz - pz;
-        const float gdist = fmaxf(ob_norm3(gx, gy, gz), 1.0f);
-        const float desired_yaw_b = atan2f(gy, gx);
-        const float gs = hypotf(vx, vy);
-        const float course_yaw = gs > 2.5f ? atan2f(vy, vx) : yaw;
-        const float course_err = ob_wrap(desired_yaw_b, course_yaw);
+    if (bwb) {
+        const float course_err = wraps.v[2];
         const float desired_speed =
             bwb_endurance ? 18.5f : (arena ? (gdist > 38.0f ? 26.0f : 24.0f) : 22.4f);
         const float speed_err = desired_speed - vb_x;
         const float u_coll = ob_clamp((bwb_endurance ? 0.36f : 0.44f) + 0.065f * speed_err +
                                           0.018f * gz, 0.12f, 0.90f);
-        const float roll_right = atan2f(r21, r22);
         const float desired_roll = ob_clamp(-1.35f * course_err, -0.55f, 0.55f);
         const float diff_u =
             ob_clamp(0.90f * (desired_roll - roll_right) - 0.34f * ox, -0.45f, 0.45f);
@@ -816,9 +879,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
         const float pitch_up = asinf(ob_clamp(r20, -1.0f, 1.0f));
         const float climb_des = ob_clamp(0.42f * gz, -5.0f, 5.0f);
         const float climb_err = climb_des - vz;
-        const SinCos bank = sin_cos(roll_right);
-        const float cos_bank = bank.c, sin_bank = bank.s;
-        const float gamma_des = atan2f(climb_des, fmaxf(gs, 14.0f));
+        const float cos_bank = cosines.v[2], sin_bank = sines.v[2];
         float desired_pitch = ob_clamp(0.062831853f + 0.75f * gamma_des + 0.035f * climb_err +
                                            0.09f * (1.0f - fmaxf(cos_bank, 0.5f)),
                                        -0.15f, 0.25f);
@@ -832,23 +893,9 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
         const float gimbal = pi / 6.0f;
         const float inner0 = ob_clamp(0.85f * (q_up + oy) + 0.03f, -gimbal, gimbal);
         const float inner1 = ob_clamp(-0.65f * (r_left - oz) - 0.025f * vb_y, -gimbal, gimbal);
-        inner_cmd = a == 0 ? inner0 : (a == 1 ? inner1 : 0.0f);
+        inner_cmd = quad_pick(a, inner0, inner1, 0.0f, 0.0f);
         outer_cmd = 0.0f;
-        const float oppx = brx - vx * 0.10f, oppy = bry - vy * 0.10f, oppz = brz - vz * 0.10f;
-        const float bdist = fmaxf(ob_norm3(oppx, oppy, oppz), 1.0f);
-        const bool head_on = bwb_arena && btx * px + bty * py < -800.0f && bdist > 45.0f;
-        const float closing = head_on ? 75.0f + 2.0f * fmaxf(vb_x, 0.0f) : 75.0f;
-        const float bflight = bdist / closing;
-        const float bax = oppx, bay = oppy;
-        const float baz =
-            oppz + (head_on ? -vz * (0.85f * bflight) : 0.0f) + 0.50f * gravity * bflight * bflight;
-        const float bbx = r00 * bax + r10 * bay + r20 * baz;
-        const float bby = r01 * bax + r11 * bay + r21 * baz;
-        const float bbz = r02 * bax + r12 * bay + r22 * baz;
-        const float b_az = ob_clamp(atan2f(bby, fmaxf(bbx, 0.2f)), -pi / 6.0f, pi / 6.0f);
-        const float b_el = ob_clamp(atan2f(bbz, fmaxf(hypotf(bbx, bby), 0.2f)), -cannon_el_lim,
-                                    cannon_el_lim);
-        const float b_err = hypotf(ob_wrap(b_az, o[44]), b_el - o[45]);
+        const float b_err = hypotf(wraps.v[3], b_el - o[45]);
         const bool b_fire = arena && o[46] <= 0.02f && o[47] > 0.01f && b_err < 0.045f &&
                             bdist < 165.0f && bbx > 0.0f;
         norm_az = arena ? ob_clamp(b_az / (pi / 6.0f), -1.0f, 1.0f) : 0.0f;
