@@ -949,17 +949,42 @@ __device__ __forceinline__ float actor_scale(int i) {  // network_gpu.cu:287-293
 
 // network_gpu.cu:285-297 (scalar_inputs): lanes 0..51 of a wave write the
 // environment's 52 symlog scalars, lanes 52..61 its 10 finite mission values.
-__device__ __forceinline__ void actor_scalars(const float *obs, const float *mission, int lane,
-                                              float *proprio, float *mission_vec) {
-    if (lane < 52) {
-        float raw = lane < 48 ? obs[lane] : obs[4144 + lane - 48];
-        raw = __builtin_isfinite(raw) ? fmaxf(-1000.0f, fminf(1000.0f, raw)) : 0.0f;
-        const float symlog = copysignf(log1p_pos(fabsf(raw * actor_scale(lane))), raw);
-        proprio[lane] = fmaxf(-8.0f, fminf(8.0f, symlog / sqrtf(1.0001f)));
-    } else if (lane < 62) {
-        const float m = mission[lane - 52];
-        mission_vec[lane - 52] = __builtin_isfinite(m) ? m : 0.0f;
-    }
+// The input of lane l is obs[l] (l < 48), obs[4144 + l - 48] (l < 52) or
+// mission[l - 52] (l < 62); it is requested one environment ahead, through
+// buffer resources (0 bytes when there is no such environment), so that its
+// round trip overlaps that environment's scan.
+constexpr unsigned kMissionRowBytes = 10 * sizeof(float);
+constexpr int kPastRecords = 0x40000000;  // past every resource: reads 0
+
+__device__ __forceinline__ float actor_scalar_input(__amdgpu_buffer_rsrc_t obs,
+                                                    __amdgpu_buffer_rsrc_t mission, int lane) {
+    const int obs_off = lane < 48 ? 4 * lane : (lane < 52 ? 4 * (4096 + lane) : kPastRecords);
+    const int mission_off = lane >= 52 && lane < 62 ? 4 * (lane - 52) : kPastRecords;
+    const float o =
+        __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(obs, obs_off, 0, 0));
+    const float m =
+        __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(mission, mission_off, 0, 0));
+    return lane < 52 ? o : m;
+}
+
+// Branch-free: every lane forms both values, and buffer stores (discarded
+// past num_records) write lanes 0..51 into proprio and 52..61 into
+// mission_vec.  A store issued on one path only would make the compiler
+// wait for every outstanding load (the next ranges) where the paths join.
+__device__ __forceinline__ void actor_scalars(float raw, int lane, float *proprio,
+                                              float *mission_vec) {
+    const bool finite = __builtin_isfinite(raw);
+    const float clamped = finite ? fmaxf(-1000.0f, fminf(1000.0f, raw)) : 0.0f;
+    const float symlog = copysignf(log1p_pos(fabsf(clamped * actor_scale(lane))), clamped);
+    const float scaled = fmaxf(-8.0f, fminf(8.0f, symlog / sqrtf(1.0001f)));
+    __builtin_amdgcn_raw_buffer_store_b32(
+        __builtin_bit_cast(unsigned, scaled),
+        __builtin_amdgcn_make_buffer_rsrc(proprio, (short)0, 52 * 4, kBufferWord3),
+        lane < 52 ? 4 * lane : kPastRecords, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(
+        __builtin_bit_cast(unsigned, finite ? raw : 0.0f),
+        __builtin_amdgcn_make_buffer_rsrc(mission_vec, (short)0, 10 * 4, kBufferWord3),
+        lane >= 52 && lane < 62 ? 4 * (lane - 52) : kPastRecords, 0, 0);
 }
 
 // Phase 1: each wave scans one environment at a time; workgroups are
@@ -995,8 +1020,17 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
         return load_frame_obs(obs_of(e < rows.batch ? e : first));
     };
     const FrameObs first_obs = frame_obs(env);
+    auto mission_rsrc = [&](size_t e, bool valid) {
+        return __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<unsigned char *>(rows.mission + e * rows.mission_stride), (short)0,
+            valid ? (int)kMissionRowBytes : 0, kBufferWord3);
+    };
     float rg[kScanRays];
     load_ranges(obs_rsrc(obs_of(env), true), lane, rg);
+    float scalar_in = 0.0f;
+    if (SCALARS)
+        scalar_in =
+            actor_scalar_input(obs_rsrc(obs_of(env), true), mission_rsrc(env, true), lane);
     ScanFrame mine = scan_frame(first_obs);
     for (int k = 0;;) {
         ScanFrame f;
@@ -1021,10 +1055,13 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
             park[5] = __int_as_float(s.min_ray);
             park[6] = __int_as_float(s.cluster_count);
         }
-        if (SCALARS)
-            actor_scalars(obs_of(env),
-                          reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride),
-                          lane, rows.proprio + env * 91, rows.mission_vec + env * 49);
+        if (SCALARS) {
+            const float scalar_next = actor_scalar_input(
+                obs_rsrc(has_next ? obs_of(next_env) : nullptr, has_next),
+                mission_rsrc(has_next ? next_env : 0, has_next), lane);
+            actor_scalars(scalar_in, lane, rows.proprio + env * 91, rows.mission_vec + env * 49);
+            scalar_in = scalar_next;
+        }
         if (!has_next) break;
         env = next_env;
         if (++k == 64) {  // the next 64 environments of this wave
