@@ -494,6 +494,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--sets", type=int, default=3, help="rotating input buffer sets")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-threads", type=int, default=None,
+                    help="host threads of the CPU baseline (default: the host share, at most 16)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--suite", action="store_true",
                     help="also time the secondary workloads (stderr JSON lines)")
@@ -551,7 +553,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")
-        cpu = cpu_baseline(host0, threads, args.cpu_seconds)
+        cpu = cpu_baseline(host0, args.cpu_threads or threads, args.cpu_seconds)
     line = {
         "metric": METRIC,
         "value": round(BATCH / per_call, 1),
