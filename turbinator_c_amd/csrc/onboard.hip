@@ -1193,7 +1193,9 @@ extern "C" int tb_hip_onboard_tactical_prior_device(const float *obs, const floa
 // src/network/network_gpu.cu:274-304 scalar_inputs, :467-479 lidar_channels,
 // :480-483 camera_luma, launched back to back at :1446-1451).  One workgroup
 // per environment streams the LiDAR block once into the six channel planes
-// and the cameras once into luma, with 16-byte coalesced loads and stores.
+// and the cameras once into luma: LiDAR in 16-byte loads, camera bytes in
+// 4-byte loads so that each lane's 4 luma values are one float4 and every
+// store instruction writes 1 KiB of consecutive output.
 // The onboard scan waves add the 52 symlog scalars and the mission values
 // (lanes idle during the scan's set-up), the control kernel tactical / prior
 // and their copies.  Fusing the scan into the streaming launch was measured
@@ -1235,11 +1237,11 @@ __global__ __launch_bounds__(256) void actor_stream_kernel(ActorRows rows) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) v[k] = __builtin_nontemporal_load(lidar + t + 256 * k);
         }
-        u32x4 px[4];
+        unsigned px[16];
         if (rows.luma) {
-            const u32x4 *cam = reinterpret_cast<const u32x4 *>(rows.cameras + env * 16384);
+            const unsigned *cam = reinterpret_cast<const unsigned *>(rows.cameras + env * 16384);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) px[k] = __builtin_nontemporal_load(cam + t + 256 * k);
+            for (int k = 0; k < 16; ++k) px[k] = __builtin_nontemporal_load(cam + t + 256 * k);
         }
         if (rows.lidar) {
             // float4 j = t + 256k of the block is bins 4(j%512).. of head j/512;
@@ -1256,18 +1258,13 @@ __global__ __launch_bounds__(256) void actor_stream_kernel(ActorRows rows) {
         if (rows.luma) {
             f32x4 *dst = reinterpret_cast<f32x4 *>(rows.luma + env * 16384);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int j = t + 256 * k;
+            for (int k = 0; k < 16; ++k) {
+                const unsigned w = px[k];
+                f32x4 o;
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const unsigned w = px[k][d];
-                    f32x4 o;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        o[e] = __builtin_fmaf((float)((w >> (8 * e)) & 0xffu), 1.0f / 255.0f,
-                                              -0.5f);
-                    dst[4 * j + d] = o;
-                }
+                for (int e = 0; e < 4; ++e)
+                    o[e] = __builtin_fmaf((float)((w >> (8 * e)) & 0xffu), 1.0f / 255.0f, -0.5f);
+                dst[t + 256 * k] = o;
             }
         }
     }
