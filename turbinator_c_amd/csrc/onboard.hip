@@ -1196,9 +1196,9 @@ extern "C" int tb_hip_onboard_tactical_prior_device(const float *obs, const floa
 // and the cameras once into luma: LiDAR in 16-byte loads, camera bytes in
 // 4-byte loads so that each lane's 4 luma values are one float4 and every
 // store instruction writes 1 KiB of consecutive output.
-// The onboard scan waves add the 52 symlog scalars and the mission values
-// (lanes idle during the scan's set-up), the control kernel tactical / prior
-// and their copies.  Fusing the scan into the streaming launch was measured
+// The onboard scan wave of each environment adds its 52 symlog scalars and
+// mission values after the scan, the control kernel tactical / prior and
+// their copies.  Fusing the scan into the streaming launch was measured
 // slower: next to saturated HBM traffic the scan's dependent loads stall.  Luma is
 // one fused multiply-add, which is what nvcc's default --fmad=true makes of
 // the reference's `(float)b * (1.0f / 255.0f) - 0.5f`.
