@@ -146,6 +146,41 @@ def test_without_diag_and_sizes(torch_cuda, hip):
         assert np.abs(tac - wt).max() <= TOL and np.abs(pri - wp).max() <= TOL
 
 
+def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
+    """The scan grid has 4,096 waves; each forms the frames of its next 64
+    environments at once, so a batch beyond 64 x 4,096 makes the first waves
+    form a second group.  4,096 distinct environments are tiled on the device
+    to 263,144 rows (4.4 GB of observations); every row must equal, bit for
+    bit, the same environment's row from the 4,096-row call."""
+    torch = torch_cuda
+    distinct, batch = 4096, 64 * 4096 + 1000
+    note(f"onboard {batch} envs tiled from {distinct} (second frame group)")
+    b = synth.make_batch(distinct, seed=271, threads=16)
+    obs = torch.from_numpy(in_window(b.obs)).cuda()
+    mission = torch.from_numpy(b.mission).cuda()
+    reps = (batch + distinct - 1) // distinct
+    big_obs = obs.repeat(reps, 1)[:batch].contiguous()
+    big_mis = mission.repeat(reps, 1)[:batch].contiguous()
+
+    def run(o, m):
+        n = o.shape[0]
+        tac = torch.full((n, 24), float("nan"), dtype=torch.float32, device="cuda")
+        pri = torch.full((n, 15), float("nan"), dtype=torch.float32, device="cuda")
+        diag = torch.full((n, 4), float("nan"), dtype=torch.float32, device="cuda")
+        s = torch.cuda.current_stream()
+        assert hip.onboard_tactical_prior_device(o, m, tac, pri, diag, n, s) == 1
+        assert hip.synchronize(s) == 1
+        return [t.cpu().numpy().view(np.uint32) for t in (tac, pri, diag)]
+
+    small = run(obs, mission)
+    big = run(big_obs, big_mis)
+    del big_obs, big_mis
+    rows = np.arange(batch) % distinct
+    for g, w, name in zip(big, small, ("tactical", "prior", "diag")):
+        bad = np.argwhere((g != w[rows]).any(1)).ravel()
+        assert not bad.size, f"{name} differs at rows {bad[:5]}"
+
+
 def test_argument_validation(hip):
     lib = hip.hip_lib()
     import ctypes
