@@ -248,27 +248,37 @@ template <int LV, int CV, bool DIAG, bool DEPTH = false>
 __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
     __shared__ f32x4 stage[16 * kStagePitch];
     // DIAG partials per (chunk, sector): minimum valid range and
-    // (first argmin bin + 1) | (valid count << 16).
-    __shared__ float dmin[DIAG ? 16 * kStagePitch : 1];
-    __shared__ unsigned dinfo[DIAG ? 16 * kStagePitch : 1];
-    const int lane = threadIdx.x & 63;
+    // (position of its first occurrence among the chunk's 4 bins, 1-based,
+    // 0 if none) | (valid count << 16).  One 8-byte slot per (chunk, sector),
+    // so that wave 0 reads them at 16-bit immediate offsets from one address
+    // register; wave 0 turns positions into bin indices.
+    __shared__ u32x2 dpart[DIAG ? 16 * kStagePitch : 1];
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool has_cameras = DEPTH || rows.cameras != nullptr;
 
-    // Stage position of this lane's float4 for each of the wave's 4 loads:
-    // LiDAR float4 index i*64 + lane (i = 4w + k) is row (i%8)*2 + lane/32
-    // of head i/8, azimuth sector (lane%32)/4, bins 4*(lane%4)..+3.
-    int unit[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const int i = 4 * w + k, head = i >> 3, row = ((i & 7) << 1) + (lane >> 5);
-        const int sector = head * 32 + (row >> 2) * 8 + ((lane & 31) >> 2);
-        const int chunk = (row & 3) * 4 + (lane & 3);
-        unit[k] = chunk * kStagePitch + sector;
-    }
-
     for (size_t env = xcd_contiguous(blockIdx.x, gridDim.x); env < rows.batch;
          env += gridDim.x) {
+        // With DIAG the lane index passes through an empty asm once per
+        // environment, so the values derived from it (addresses, stage
+        // positions, bin offsets) are formed per environment instead of
+        // being hoisted out of this loop, which nearly always runs once,
+        // into registers held across it: 64 instead of 100 VGPRs, 6 instead
+        // of 4 waves per SIMD.  The other variants keep the hoisted form
+        // (7 waves per SIMD measured faster than 8 there).
+        int lane = threadIdx.x & 63;
+        if constexpr (DIAG) asm volatile("" : "+v"(lane));
+        // Stage position of this lane's float4 for each of the wave's 4
+        // loads: LiDAR float4 index i*64 + lane (i = 4w + k) is row
+        // (i%8)*2 + lane/32 of head i/8, azimuth sector (lane%32)/4, bins
+        // 4*(lane%4)..+3.
+        int unit[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * w + k, head = i >> 3, row = ((i & 7) << 1) + (lane >> 5);
+            const int sector = head * 32 + (row >> 2) * 8 + ((lane & 31) >> 2);
+            const int chunk = (row & 3) * 4 + (lane & 3);
+            unit[k] = chunk * kStagePitch + sector;
+        }
         float *out = rows.out + env * kFeatureDim;
         size_t src = env;
         if (rows.index) {
@@ -309,25 +319,21 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
             f.z = lidar_bin_term(v[k].z);
             f.w = lidar_bin_term(v[k].w);
             stage[unit[k]] = f;
-        }
-        if constexpr (DIAG) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int i = 4 * w + k;
-                const int bin0 = (i >> 3) * 2048 + (((i & 7) << 1) + (lane >> 5)) * 128 +
-                                 ((lane & 31) >> 2) * 16 + 4 * (lane & 3);
+            if constexpr (DIAG) {
+                // Bins in increasing order, so a strict < keeps the first
+                // minimum; selects rather than branches.
                 float best = 0.0f;
                 unsigned first = 0u, count = 0u;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float r = v[k][e];
-                    if ((r >= 0.0f) && (r < __builtin_huge_valf())) {
-                        ++count;
-                        if (first == 0u || r < best) { best = r; first = bin0 + e + 1; }
-                    }
+                    const bool valid = (int)(r >= 0.0f) & (int)(r < __builtin_huge_valf());
+                    const bool take = (int)valid & ((int)(first == 0u) | (int)(r < best));
+                    count += valid ? 1u : 0u;
+                    best = take ? r : best;
+                    first = take ? (unsigned)(e + 1) : first;
                 }
-                dmin[unit[k]] = best;
-                dinfo[unit[k]] = first | (count << 16);
+                dpart[unit[k]] = u32x2{__float_as_uint(best), first | (count << 16)};
             }
         }
 
@@ -367,22 +373,7 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
         } else if (lane < 4) {
             out[126 + w * 4 + lane] = 0.0f;
         }
-        if (w == 1 && lane < 62) {
-            // training.c:107-112.
-            float scalar;
-            if (lane < 48) {
-                scalar = clamp_ref(finite_or_zero(sv) / scalar_scale(lane), -1.0f, 1.0f);
-            } else if (lane < 52) {
-                scalar = clamp_ref(finite_or_zero(sv), 0.0f, 1.0f);
-            } else {
-                const int i = lane - 52;
-                const bool arena = finite_or_zero(m6) > 0.5f;
-                const float m = (i >= 7 && arena) ? 0.0f : sv;
-                scalar = clamp_ref(finite_or_zero(m), -1.0f, 1.0f);
-            }
-            out[lane] = scalar;
-        }
-        if constexpr (DIAG) {
+        if constexpr (DIAG) {  // camera words are dead after this
             uint32_t *diag = rows.diag + env * 224;
             if (has_cameras) {
                 const unsigned top_min = min_same_qx(bytes_min(px[1], bytes_min(px[0], 255u)));
@@ -402,6 +393,21 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
             }
         }
 
+        if (w == 1 && lane < 62) {
+            // training.c:107-112.
+            float scalar;
+            if (lane < 48) {
+                scalar = clamp_ref(finite_or_zero(sv) / scalar_scale(lane), -1.0f, 1.0f);
+            } else if (lane < 52) {
+                scalar = clamp_ref(finite_or_zero(sv), 0.0f, 1.0f);
+            } else {
+                const int i = lane - 52;
+                const bool arena = finite_or_zero(m6) > 0.5f;
+                const float m = (i >= 7 && arena) ? 0.0f : sv;
+                scalar = clamp_ref(finite_or_zero(m), -1.0f, 1.0f);
+            }
+            out[lane] = scalar;
+        }
         __syncthreads();
         if (w == 0) {
             // training.c:113-127: sequential sum, row outer, bin inner.
@@ -416,19 +422,28 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
             }
             out[62 + lane] = sum / 64.0f;
             if constexpr (DIAG) {
+                // After the sums (a scheduling fence keeps the 32 partials'
+                // LDS reads from being hoisted next to the 16 staged float4,
+                // which would cost two waves per SIMD of registers).
+                __builtin_amdgcn_sched_barrier(0);
                 // Chunks in increasing c are in scan order (row outer, bin
                 // inner), so a strict < keeps the first minimum.
+                // Sector `lane` (head, elevation sector, azimuth sector);
+                // chunk c holds its elevation row 4 es + c / 4, bins
+                // 4 (c % 4) .. + 3 of the azimuth sector.
+                const unsigned sector_bin0 =
+                    (lane >> 5) * 2048 + ((lane >> 3) & 3) * 512 + (lane & 7) * 16;
                 float best = 0.0f;
                 unsigned first = 0u, count = 0u;
 #pragma unroll
                 for (int c = 0; c < 16; ++c) {
-                    const unsigned info = dinfo[c * kStagePitch + lane];
-                    const float m = dmin[c * kStagePitch + lane];
-                    count += info >> 16;
-                    if ((info & 0xffffu) != 0u && (first == 0u || m < best)) {
-                        best = m;
-                        first = info & 0xffffu;
-                    }
+                    const u32x2 part = dpart[c * kStagePitch + lane];
+                    const unsigned pos = part.y & 0xffffu;
+                    const float m = __uint_as_float(part.x);
+                    count += part.y >> 16;
+                    const bool take = (int)(pos != 0u) & ((int)(first == 0u) | (int)(m < best));
+                    best = take ? m : best;
+                    first = take ? sector_bin0 + (c >> 2) * 128 + 4 * (c & 3) + pos : first;
                 }
                 uint32_t *diag = rows.diag + env * 224;
                 diag[lane] = first == 0u ? __float_as_uint(-1.0f) : __float_as_uint(best);
