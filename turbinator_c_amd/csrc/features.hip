@@ -422,10 +422,6 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
             }
             out[62 + lane] = sum / 64.0f;
             if constexpr (DIAG) {
-                // After the sums (a scheduling fence keeps the 32 partials'
-                // LDS reads from being hoisted next to the 16 staged float4,
-                // which would cost two waves per SIMD of registers).
-                __builtin_amdgcn_sched_barrier(0);
                 // Chunks in increasing c are in scan order (row outer, bin
                 // inner), so a strict < keeps the first minimum.
                 // Sector `lane` (head, elevation sector, azimuth sector);
