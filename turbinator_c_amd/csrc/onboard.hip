@@ -174,38 +174,14 @@ struct RayPlanes {
     float d[3][1536];
 };
 
-// Closest-return key: (range bits << 32) | ray.  Ranges that can win are
-// positive, so unsigned order on the key is the (range, ray) order.
-constexpr uint64_t kNoReturnKey = (uint64_t)0x41f00000u << 32 | 0x7fffffffu;  // (30.0f, none)
-
-template <int CTRL>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-    const unsigned lo = (unsigned)dpp_partner<CTRL>((int)(unsigned)v);
-    const unsigned hi = (unsigned)dpp_partner<CTRL>((int)(unsigned)(v >> 32));
-    return (uint64_t)hi << 32 | lo;
-}
-
-template <bool SWAP32>
-__device__ __forceinline__ uint64_t swap_min_u64(uint64_t v) {
-    int olo, ohi;
-    const unsigned lo = (unsigned)swap_pair<SWAP32>((int)(unsigned)v, olo);
-    const unsigned hi = (unsigned)swap_pair<SWAP32>((int)(unsigned)(v >> 32), ohi);
-    const uint64_t a = (uint64_t)hi << 32 | lo;
-    const uint64_t b = (uint64_t)(unsigned)ohi << 32 | (unsigned)olo;
-    return b < a ? b : a;
-}
-
-__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-    uint64_t p = dpp_u64<0xB1>(v);
-    v = p < v ? p : v;
-    p = dpp_u64<0x4E>(v);
-    v = p < v ? p : v;
-    p = dpp_u64<0x141>(v);
-    v = p < v ? p : v;
-    p = dpp_u64<0x140>(v);
-    v = p < v ? p : v;
-    v = swap_min_u64<false>(v);
-    return swap_min_u64<true>(v);
+__device__ __forceinline__ unsigned wave_min_u32(unsigned v) {
+    v = min(v, (unsigned)dpp_partner<0xB1>((int)v));
+    v = min(v, (unsigned)dpp_partner<0x4E>((int)v));
+    v = min(v, (unsigned)dpp_partner<0x141>((int)v));
+    v = min(v, (unsigned)dpp_partner<0x140>((int)v));
+    int o;
+    v = min((unsigned)swap_pair<false>((int)v, o), (unsigned)o);
+    return min((unsigned)swap_pair<true>((int)v, o), (unsigned)o);
 }
 
 // Buffer resources (gfx9 word 3): loads read zero past num_records instead
@@ -268,11 +244,13 @@ __device__ __forceinline__ ScanFrame scan_frame(FrameObs v) {
 // lane, no workgroup barrier).
 //   * The reference maps non-finite ranges to 0 / +-1000 first; both fail
 //     the 0.35 < r < 11.5 window, as NaN does, so the raw value is tested.
-//   * The closest return is the minimum (range, ray) key over elevation rows
-//     0..3: the key order breaks range ties by ray index, so the result is
-//     the reference's first minimum in scan order.  Lane 0 recomputes the
-//     winner's world offset with the reference's expression, which gives the
-//     value pass 1 formed (see the pair identity below).
+//   * The closest return over elevation rows 0..3 is found in two steps: the
+//     wave's minimum in-window range (as bits: positive floats order like
+//     their bit patterns), then the first slot in ray order and the first
+//     lane holding exactly that range, from lane masks on the scalar unit.
+//     That is the reference's first minimum in scan order.  Lane 0
+//     recomputes the winner's world offset with the reference's expression,
+//     which gives the value pass 1 formed (see the pair identity below).
 //   * Pass 1 is branch-free and keeps each ray's corridor centre (x = +inf
 //     outside the window or the corridor), so pass 2 is a compare-and-add.
 //   * Once pass 1 has consumed the ranges, the registers take the next
@@ -282,21 +260,27 @@ __device__ __forceinline__ ScanFrame scan_frame(FrameObs v) {
 __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes &rays,
                                          const ScanFrame &f, __amdgpu_buffer_rsrc_t next,
                                          int lane, ScanResult &out) {
-    // Closest-return candidate of this lane, in ray order (strict <).
-    // Starting the running best at 11.5 folds the window's upper bound into
-    // that compare.
-    float best_r = 11.5f;
-    int best_u = -1;
+    // Closest return.  A slot outside the window counts as 11.5, the
+    // window's exclusive upper bound, so it never wins.
+    constexpr unsigned kWindowTop = 0x41380000u;  // 11.5f
+    unsigned lane_min = kWindowTop;
 #pragma unroll
     for (int u = 0; u < kScanRays; ++u) {
         if ((u / 2) % 6 >= 4) continue;
-        const bool take = (int)(rg[u] > 0.35f) & (int)(rg[u] < best_r);
-        best_r = take ? rg[u] : best_r;
-        best_u = take ? u : best_u;
+        lane_min = min(lane_min, rg[u] > 0.35f ? __float_as_uint(rg[u]) : kWindowTop);
     }
-    uint64_t key = kNoReturnKey;
-    if (best_u >= 0)
-        key = (uint64_t)__float_as_uint(best_r) << 32 | (unsigned)(64 * best_u + lane);
+    const unsigned min_bits = wave_min_u32(lane_min);
+    int min_ray = -1;
+    if (min_bits != kWindowTop) {
+        // Visiting slots from the last to the first leaves the first slot
+        // (in ray order) that holds the range, at its first lane.
+#pragma unroll
+        for (int u = kScanRays - 1; u >= 0; --u) {
+            if ((u / 2) % 6 >= 4) continue;
+            const uint64_t hit = __builtin_amdgcn_ballot_w64(__float_as_uint(rg[u]) == min_bits);
+            if (hit) min_ray = 64 * u + (int)__builtin_ctzll(hit);
+        }
+    }
 
     // Pass 1.  The rays of rows el and el + 6 (heads 0 and 1) at the same
     // azimuth have the same table x, y and the negated z, bit for bit.  With
@@ -331,13 +315,14 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
                                       (int)(x_center <= 10.5f) & (int)(fabsf(y_center) <= 3.5f);
                 xc[u] = corridor ? x_center : __builtin_huge_valf();
                 yc[u] = y_center;
-                min_dx_c = (int)corridor & (int)(x_center < min_dx_c) ? x_center : min_dx_c;
+                // The reference's strict-< update over corridor rays is the
+                // minimum of their centres (+inf elsewhere): exact.
+                min_dx_c = fminf(min_dx_c, xc[u]);
             }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
     load_ranges(next, lane, rg);
-    key = wave_min_u64(key);
     min_dx_c = wave_min(min_dx_c);
 
     // Pass 2: the cluster is counted from the lane masks (scalar unit); y is
@@ -356,13 +341,13 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
     }
     y_sum = wave_sum_double(y_sum);
     if (lane == 0) {
-        const int ray = (int)(unsigned)key;
-        const float range = __uint_as_float((unsigned)(key >> 32));
+        const int ray = min_ray;
+        const float range = min_ray >= 0 ? __uint_as_float(min_bits) : 30.0f;
         out.min_r = range;
         out.min_r_dx = 0.0f;
         out.min_r_dy = 0.0f;
         out.min_ray = -1;
-        if (ray != 0x7fffffff) {
+        if (ray >= 0) {
             const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
             const float rwx = f.r[0] * dx + f.r[1] * dy + f.r[2] * dz;
             const float rwy = f.r[3] * dx + f.r[4] * dy + f.r[5] * dz;
