@@ -463,14 +463,16 @@ def cpu_baseline(host0, threads: int, budget_s: float) -> dict:
                 host0.cameras.ctypes.data, CAMERA_B, out.ctypes.data, sample, threads)
         run = lambda: lib.orc_features_batch(*args)  # noqa: E731
     run()  # warm-up pass
-    envs, t0 = 0, time.perf_counter()
+    envs, t0, rates = 0, time.perf_counter(), []
     while True:
+        tp = time.perf_counter()
         run()
+        rates.append(sample / (time.perf_counter() - tp))
         envs += sample
         el = time.perf_counter() - t0
         if el >= budget_s:
             break
-    rate = envs / el
+    rate = float(np.median(rates))  # median of the timed passes
     cpu = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -482,9 +484,9 @@ def cpu_baseline(host0, threads: int, budget_s: float) -> dict:
     what = ("the reference's tb_train_extract_features_cpu" if kind == "reference"
             else "the oracle restatement of tb_train_extract_features_cpu")
     return {"value": round(rate, 1), "unit": "envs/s", "cores": threads, "kind": kind,
-            "sample": f"{what} over {envs} envs ({sample}-env slices of the configuration-3 "
-                      f"batch, {el:.1f} s) on {threads} threads of {cpu}; "
-                      f"{rate * BYTES_PER_ENV / 1e9:.2f} GB/s effective"}
+            "sample": f"{what}: median of {len(rates)} timed passes over {sample}-env slices "
+                      f"of the configuration-3 batch ({envs} envs, {el:.1f} s) on {threads} "
+                      f"threads of {cpu}; {rate * BYTES_PER_ENV / 1e9:.2f} GB/s effective"}
 
 
 def main() -> int:
