@@ -152,34 +152,62 @@ constexpr int kGroups = 2;  // groups of 16 environments per workgroup pass
 constexpr int kDepth = 4;
 constexpr unsigned kPastEnd = 0x80000000u;  // lane offset beyond any packed buffer
 
-template <int KC, int NT, int TPW, int G, bool TANH, int S>
-__device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
-                                            unsigned b_off, const f32x4 *rows,
-                                            f32x4 (&out)[TPW][G], int w, int lane) {
-    const int g = lane >> 4;
-    const f32x4 *in = rows + ((lane & 15) * S) / 4 + g;  // group q, chunk s: in[q 4S + 4 s]
-    unsigned wl[TPW], bl[TPW];
-    int nt[TPW];
+// The first kDepth - 1 weight chunks and the bias of this wave's tiles of one
+// layer, requested ahead of the layer (layer_prefetch) so that their round
+// trip overlaps the previous phase of the pass.
+template <int TPW>
+struct LayerWeights {
+    f32x4 ring[kDepth][TPW];
+    f32x4 bias[TPW];
+};
+
+// Lane offsets of this wave's tile slots: a slot past the layer's NT tiles
+// reads at kPastEnd (zeros through the buffer resource).
+template <int NT, int TPW>
+__device__ __forceinline__ void tile_slots(int w, int lane, unsigned (&wl)[TPW],
+                                           unsigned (&bl)[TPW], int (&nt)[TPW]) {
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
         nt[j] = w + kWaves * j;
         const bool valid = nt[j] < NT;
         wl[j] = valid ? 16u * lane : kPastEnd;
-        bl[j] = valid ? 16u * g : kPastEnd;
+        bl[j] = valid ? 16u * (lane >> 4) : kPastEnd;
         if (!valid) nt[j] = 0;
     }
-    f32x4 acc[TPW][G], ring[kDepth][TPW], bias[TPW];
+}
+
+template <int KC, int NT, int TPW>
+__device__ __forceinline__ void layer_prefetch(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
+                                               unsigned b_off, int w, int lane,
+                                               LayerWeights<TPW> &lw) {
+    unsigned wl[TPW], bl[TPW];
+    int nt[TPW];
+    tile_slots<NT, TPW>(w, lane, wl, bl, nt);
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
-#pragma unroll
-        for (int q = 0; q < G; ++q) acc[j][q] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-        bias[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, bl[j], b_off + 64u * nt[j], 0);
+        lw.bias[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, bl[j], b_off + 64u * nt[j], 0);
 #pragma unroll
         for (int d = 0; d < kDepth - 1; ++d)
             if (d < KC)
-                ring[d][j] = __builtin_amdgcn_raw_buffer_load_b128(
+                lw.ring[d][j] = __builtin_amdgcn_raw_buffer_load_b128(
                     rsrc, wl[j], w_off + 1024u * (nt[j] * KC + d), 0);
     }
+}
+
+template <int KC, int NT, int TPW, int G, bool TANH, int S>
+__device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
+                                            const f32x4 *rows, LayerWeights<TPW> &lw,
+                                            f32x4 (&out)[TPW][G], int w, int lane) {
+    const int g = lane >> 4;
+    const f32x4 *in = rows + ((lane & 15) * S) / 4 + g;  // group q, chunk s: in[q 4S + 4 s]
+    unsigned wl[TPW], bl[TPW];
+    int nt[TPW];
+    tile_slots<NT, TPW>(w, lane, wl, bl, nt);
+    f32x4 acc[TPW][G];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+        for (int q = 0; q < G; ++q) acc[j][q] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 xc[G], xn[G];
 #pragma unroll
     for (int q = 0; q < G; ++q) xn[q] = xc[q] = in[q * 4 * S];
@@ -188,7 +216,7 @@ __device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigne
         if (s + kDepth - 1 < KC) {
 #pragma unroll
             for (int j = 0; j < TPW; ++j)
-                ring[(s + kDepth - 1) % kDepth][j] = __builtin_amdgcn_raw_buffer_load_b128(
+                lw.ring[(s + kDepth - 1) % kDepth][j] = __builtin_amdgcn_raw_buffer_load_b128(
                     rsrc, wl[j], w_off + 1024u * (nt[j] * KC + s + kDepth - 1), 0);
         }
         if (s + 1 < KC) {
@@ -202,7 +230,7 @@ __device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigne
 #pragma unroll
                 for (int q = 0; q < G; ++q)
                     acc[j][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                        ring[s % kDepth][j][t], xc[q][t], acc[j][q], 0, 0, 0);
+                        lw.ring[s % kDepth][j][t], xc[q][t], acc[j][q], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int q = 0; q < G; ++q) xc[q] = xn[q];
@@ -213,7 +241,7 @@ __device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigne
         for (int q = 0; q < G; ++q)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float y = acc[j][q][v] + bias[j][v];
+                const float y = acc[j][q][v] + lw.bias[j][v];
                 out[j][q][v] = TANH ? tanh_hidden(y) : y;
             }
 }
@@ -285,6 +313,10 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
                                    frs, (unsigned)(e * kFeatures + k) * 4, 0, 0));
             }
         }
+        // Layer 0's first weight chunks and bias, requested with the
+        // features so that both round trips overlap.
+        LayerWeights<TPW> lw0;
+        layer_prefetch<kFeatureChunks, HT, TPW>(wrs, a.w_off[0], a.b_off[0], w, lane, lw0);
         // The normal draws of this thread's (environment, action) slots
         // p = tid + 256 r, loaded now and used after the three layers.
         float drawn[kSlots];
@@ -309,23 +341,28 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
         }
         __syncthreads();
 
+        // Each layer's first weight chunks are requested before the
+        // barrier that ends the previous layer.
+        LayerWeights<TPW> lw1;
         {
             f32x4 h[TPW][G];
-            layer_tiles<kFeatureChunks, HT, TPW, G, true, S>(wrs, a.w_off[0], a.b_off[0], buf[1],
-                                                             h, w, lane);
+            layer_tiles<kFeatureChunks, HT, TPW, G, true, S>(wrs, a.w_off[0], buf[1], lw0, h, w,
+                                                             lane);
+            layer_prefetch<HT, HT, TPW>(wrs, a.w_off[1], a.b_off[1], w, lane, lw1);
             store_tiles<TPW, G, HT, S>(buf[0], h, w, lane);
         }
         __syncthreads();
+        LayerWeights<1> lw2;
         {
             f32x4 h[TPW][G];
-            layer_tiles<HT, HT, TPW, G, true, S>(wrs, a.w_off[1], a.b_off[1], buf[0], h, w,
-                                                 lane);
+            layer_tiles<HT, HT, TPW, G, true, S>(wrs, a.w_off[1], buf[0], lw1, h, w, lane);
+            if (w < 2) layer_prefetch<HT, 2, 1>(wrs, a.w_off[2], a.b_off[2], w, lane, lw2);
             store_tiles<TPW, G, HT, S>(buf[1], h, w, lane);
         }
         __syncthreads();
         if (w < 2) {
             f32x4 r[1][G];
-            layer_tiles<HT, 2, 1, G, false, S>(wrs, a.w_off[2], a.b_off[2], buf[1], r, w, lane);
+            layer_tiles<HT, 2, 1, G, false, S>(wrs, a.w_off[2], buf[1], lw2, r, w, lane);
 #pragma unroll
             for (int q = 0; q < G; ++q) {
                 const size_t env = base + 16 * q + j;
