@@ -155,6 +155,40 @@ def test_config_16384(torch_cuda, hip):
     check_h2(sub, want, "16384")
 
 
+def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
+    """As for the onboard entry: 263,144 rows tiled from 4,096 distinct
+    environments (the scan waves form a second group of 64 frames and carry
+    the symlog inputs one environment ahead across it); proprio, mission,
+    tactical and prior rows must equal the 4,096-row call's bit for bit.
+    The plane outputs are left out (they do not depend on the scan)."""
+    torch = torch_cuda
+    distinct, batch = 4096, 64 * 4096 + 1000
+    note(f"actor inputs {batch} envs tiled from {distinct}")
+    b = synth.make_batch(distinct, seed=272, threads=16)
+    obs = torch.from_numpy(b.obs).cuda()
+    mission = torch.from_numpy(b.mission).cuda()
+    reps = (batch + distinct - 1) // distinct
+
+    def run(o, m):
+        n = o.shape[0]
+        out = [torch.full((n, w), float("nan"), dtype=torch.float32, device="cuda")
+               for w in (91, 49, 24, 15)]
+        s = torch.cuda.current_stream()
+        assert hip.actor_inputs_device(o, m, None, *out, None, None, n, s) == 1
+        assert hip.synchronize(s) == 1
+        return [t.cpu().numpy().view(np.uint32) for t in out]
+
+    small = run(obs, mission)
+    big_obs = obs.repeat(reps, 1)[:batch].contiguous()
+    big_mis = mission.repeat(reps, 1)[:batch].contiguous()
+    big = run(big_obs, big_mis)
+    del big_obs, big_mis
+    rows = np.arange(batch) % distinct
+    for g, w, name in zip(big, small, ("proprio", "mission", "tactical", "prior")):
+        bad = np.argwhere((g != w[rows]).any(1)).ravel()
+        assert not bad.size, f"{name} differs at rows {bad[:5]}"
+
+
 def test_argument_validation(hip):
     lib = hip.hip_lib()
     d = ctypes.c_void_p(256)
