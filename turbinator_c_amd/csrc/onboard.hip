@@ -46,6 +46,10 @@ constexpr int kControlThreads = 320;  // wave 0 tactical, waves 1..4 controller
 constexpr int kScanRays = 1536 / 64;  // rays per lane: one wave scans one environment
 constexpr unsigned kMaxBlocks = 1u << 20;
 constexpr unsigned kScanBlocks = 256 * 4;   // persistent scan grid: 4 per CU
+// Controller grid cap: 4,096 workgroups of 64 environments.  One workgroup is
+// resident per CU (205 VGPRs), so the cap is 16 full rounds of the chip and
+// larger batches stride; a 16,384-environment call launches 256.
+constexpr unsigned kControlBlocks = 4096;
 constexpr size_t kMaxBatch = 0x7fffffffu;
 constexpr float kPi = 3.14159265358979323846f;
 
@@ -1146,7 +1150,7 @@ int launch_onboard(const OnboardRows &rows, hipStream_t s) {
         onboard_scan_kernel<true><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
     else
         onboard_scan_kernel<false><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
-    onboard_control_kernel<<<ctrl_want > kMaxBlocks ? kMaxBlocks : (unsigned)ctrl_want,
+    onboard_control_kernel<<<ctrl_want > kControlBlocks ? kControlBlocks : (unsigned)ctrl_want,
                              kControlThreads, 0, s>>>(rows);
     return hipGetLastError() == hipSuccess;
 }
