@@ -367,3 +367,37 @@ def test_indexed_aos_records(torch_cuda, hip):
                                                s) == 1
     assert hip.synchronize(s) == 1
     assert_feature_parity(out.cpu().numpy(), full[idx], "indexed-aos")
+
+
+@pytest.mark.parametrize("batch", [1, 2, 5, 63, 65, 257])
+def test_ragged_batches_every_entry(torch_cuda, hip, batch):
+    """Batches that are not a multiple of the 8 XCDs (the workgroup-to-
+    environment mapping falls back to the identity for the last ids) through
+    the device, diagnostics, depth, strided and indexed entries."""
+    note(f"ragged batch {batch}: every feature entry")
+    torch = torch_cuda
+    b = synth.make_batch(batch, seed=900 + batch, variant=synth.EDGE_QUARTERS if batch > 3 else
+                         synth.ORDINARY, with_depth=True)
+    want = oracle.features(b.obs, b.mission, b.cameras)
+    assert_feature_parity(run_device(torch, hip, b.obs, b.mission, b.cameras), want, "device")
+    feats, diag = run_diag(torch, hip, b.obs, b.mission, b.cameras)
+    assert_feature_parity(feats, want, "diagnostics")
+    assert np.array_equal(diag, oracle.diagnostics(b.obs, b.cameras))
+    assert_feature_parity(run_depth(torch, hip, b.obs, b.mission, b.depth),
+                          oracle.features(b.obs, b.mission, oracle.depth_to_luma(b.depth)),
+                          "depth")
+    strided_case(torch, hip, batch, RECORD, OFF_NEXT_OBS, OFF_NEXT_MISSION, OFF_NEXT_CAM,
+                 "strided")
+    # Indexed: every environment once, in reverse order, plus one invalid row.
+    idx = np.concatenate([np.arange(batch)[::-1], [batch]]).astype(np.uint32)
+    d_obs, d_mis = torch.from_numpy(b.obs).cuda(), torch.from_numpy(b.mission).cuda()
+    d_cam = torch.from_numpy(b.cameras).cuda()
+    d_idx = torch.from_numpy(idx.view(np.int32)).cuda()
+    out = torch.zeros((idx.size, 142), dtype=torch.float32, device="cuda")
+    s = torch.cuda.current_stream()
+    assert hip.extract_features_indexed_device(d_obs, 16592, d_mis, 40, d_cam, 16384, batch,
+                                               d_idx, out, idx.size, s) == 1
+    assert hip.synchronize(s) == 1
+    got = out.cpu().numpy()
+    assert np.all(np.isnan(got[-1]))
+    assert_feature_parity(got[:-1], want[::-1], "indexed")

@@ -33,6 +33,14 @@ struct tb_cuda_feature_batch {
     char error[192];
 };
 
+/* The device entry reads (and so clears) the launch error itself; a refused
+ * launch whose error is already cleared is reported as a launch failure
+ * rather than as "no error". */
+static hipError_t launch_status(void) {
+    const hipError_t status = hipGetLastError();
+    return status == hipSuccess ? hipErrorLaunchFailure : status;
+}
+
 static int fb_fail(tb_cuda_feature_batch *batch, const char *stage, hipError_t status) {
     snprintf(batch->error, sizeof(batch->error), "%s: %s", stage, hipGetErrorString(status));
     return 0;
@@ -96,7 +104,7 @@ int tb_cuda_extract_features_host(tb_cuda_feature_batch *batch, const float *obs
     if (status != hipSuccess) return fb_fail(batch, "copy cameras", status);
     if (!tb_cuda_extract_features_device(batch->obs, batch->mission, batch->cameras,
                                          batch->features, count, batch->stream))
-        return fb_fail(batch, "extract features", hipGetLastError());
+        return fb_fail(batch, "extract features", launch_status());
     status = hipMemcpyAsync(out_features, batch->features, count * FB_FEATURES * sizeof(float),
                             hipMemcpyDeviceToHost, batch->stream);
     if (status != hipSuccess) return fb_fail(batch, "copy features", status);

@@ -66,6 +66,14 @@ static size_t off_features(size_t n) {
     return (size_t)(FP_OBS_BYTES + FP_MISSION_BYTES + FP_CAMERA_BYTES) * n;
 }
 
+/* The device entry reads (and so clears) the launch error itself; a refused
+ * launch whose error is already cleared is reported as a launch failure
+ * rather than as "no error". */
+static hipError_t launch_status(void) {
+    const hipError_t status = hipGetLastError();
+    return status == hipSuccess ? hipErrorLaunchFailure : status;
+}
+
 static int fp_fail(tb_hip_feature_pipeline *p, const char *stage, hipError_t status) {
     snprintf(p->error, sizeof(p->error), "%s: %s", stage, hipGetErrorString(status));
     return 0;
@@ -173,7 +181,7 @@ int tb_hip_feature_pipeline_submit(tb_hip_feature_pipeline *p, int slot, size_t 
                                          with_cameras ? q->device + off_cameras(n) : NULL,
                                          (float *)(q->device + off_features(n)), count,
                                          q->stream))
-        return fp_fail(p, "extract features", hipGetLastError());
+        return fp_fail(p, "extract features", launch_status());
     status = hipMemcpyAsync(q->host + off_features(n), q->device + off_features(n),
                             count * FP_FEATURE_BYTES, hipMemcpyDeviceToHost, q->stream);
     if (status != hipSuccess) return fp_fail(p, "copy features", status);
@@ -204,7 +212,7 @@ int tb_hip_feature_pipeline_submit_direct(tb_hip_feature_pipeline *p, int slot, 
                                          with_cameras ? q->mapped + off_cameras(n) : NULL,
                                          (float *)(q->mapped + off_features(n)), count,
                                          q->stream))
-        return fp_fail(p, "extract features", hipGetLastError());
+        return fp_fail(p, "extract features", launch_status());
     q->count = count;
     q->in_flight = 1;
     return 1;
