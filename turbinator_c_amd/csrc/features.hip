@@ -185,7 +185,10 @@ __device__ __forceinline__ unsigned sum_same_qx(unsigned v) {
 // for every float x in [0, 200] (checked exhaustively by
 // tests/csrc/check_div_by_constant.c), so the bytes are bit-exact.
 __device__ __forceinline__ unsigned depth_luma(float depth_m) {
-    const float d = clamp_ref(finite_or_zero(depth_m), 0.0f, 200.0f);
+    // clamp_ref(finite_or_zero(x), 0, 200) as one median-of-three after the
+    // finiteness select: equal for every finite x (a -0.0 that may come out
+    // as +0.0 gives the same byte).
+    const float d = __builtin_amdgcn_fmed3f(finite_or_zero(depth_m), 0.0f, 200.0f);
     const float q = (float)((double)d * (1.0 / 200.0));
     return (unsigned)__builtin_rintf(255.0f * (1.0f - q));
 }
