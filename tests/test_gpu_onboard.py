@@ -98,6 +98,61 @@ def test_random_batches(torch_cuda, hip, variant, batch):
     note(f"variant {variant} stats {stats}")
 
 
+def scan_ray_columns():
+    """obs columns of the 1,536 rays the scan reads (onboard_features.cuh:189-191):
+    head h, elevation row el < 6, azimuth a -> 48 + (16 h + el) 128 + a."""
+    return np.array([48 + (16 * h + el) * 128 + a for h in range(2) for el in range(6)
+                     for a in range(128)])
+
+
+@pytest.mark.parametrize("counts", [(0, 1, 2, 63, 64, 65, 127, 128, 129, 200),
+                                    (255, 256, 257, 300, 640, 1000, 1535, 1536)])
+def test_listed_and_swept_scans(torch_cuda, hip, counts):
+    """Exactly k of an environment's 1,536 scan rays inside the 0.35..11.5 m
+    window, at random positions: up to 256 the wave lists the in-window rays
+    and runs the passes over the list, above that it sweeps every slot.  The
+    other rays take values just outside the window or non-finite ones."""
+    note(f"onboard scans with k in-window rays, k in {counts}")
+    per_k = 64
+    batch = per_k * len(counts)
+    b = synth.make_batch(batch, seed=4000 + counts[0], threads=16)
+    obs = in_window(b.obs)
+    cols = scan_ray_columns()
+    rng = np.random.default_rng(counts[-1])
+    outside = np.array([0.35, 11.5, 0.0, -0.0, -1.0, 30.0, 300.0, np.nan, np.inf, -np.inf,
+                        0.3499999, 11.500001], np.float32)
+    inside = np.array([np.nextafter(np.float32(0.35), np.float32(1)),
+                       np.nextafter(np.float32(11.5), np.float32(0))], np.float32)
+    for i, k in enumerate(counts):
+        for e in range(i * per_k, (i + 1) * per_k):
+            chosen = rng.permutation(cols.size)[:k]
+            keep = np.zeros(cols.size, bool)
+            keep[chosen] = True
+            row = obs[e]
+            vals = row[cols]
+            vals[~keep] = rng.choice(outside, (~keep).sum())
+            # a few in-window rays sit on the window's edges
+            edge = chosen[rng.random(k) < 0.05]
+            vals[edge] = rng.choice(inside, edge.size)
+            vals[keep] = np.where(np.isfinite(vals[keep]) & (vals[keep] > 0.35) &
+                                  (vals[keep] < 11.5), vals[keep], np.float32(5.0))
+            row[cols] = vals
+    got = run_onboard(torch_cuda, hip, obs, b.mission)
+    stats = compare(got, oracle.onboard(obs, b.mission), f"counts{counts}")
+    note(f"counts {counts}: {stats}")
+
+
+def test_benchmark_range_distribution(torch_cuda, hip):
+    """The generator's own ranges (uniform 0.2..300 m, 10% no-return): about
+    57 of 1,536 rays per environment fall inside the window, so every
+    environment takes the listed pass."""
+    note("onboard on the benchmark's range distribution, 4096 envs")
+    b = synth.make_batch(4096, seed=4100, threads=16)
+    got = run_onboard(torch_cuda, hip, b.obs, b.mission)
+    stats = compare(got, oracle.onboard(b.obs, b.mission), "benchmark ranges")
+    note(f"benchmark ranges: {stats}")
+
+
 def test_special_values(torch_cuda, hip):
     """NaN, +-Inf and +-0 in every field: the reference maps them (NaN -> 0,
     Inf -> +-1000 / +-1) and the geometry stays well-conditioned: strict."""

@@ -44,6 +44,10 @@ constexpr int kBlockThreads = 256;
 constexpr int kWavesPerBlock = kBlockThreads / 64;
 constexpr int kControlThreads = 320;  // wave 0 tactical, waves 1..4 controller
 constexpr int kScanRays = 1536 / 64;  // rays per lane: one wave scans one environment
+// In-window rays a wave lists for the compact pass; with more, every slot is
+// swept instead.
+constexpr int kListCap = 512;
+constexpr int kListRounds = kListCap / 64;
 constexpr unsigned kMaxBlocks = 1u << 20;
 constexpr unsigned kScanBlocks = 256 * 4;   // persistent scan grid: 4 per CU
 // Controller grid cap: 4,096 workgroups of 64 environments.  One workgroup is
@@ -244,10 +248,44 @@ __device__ __forceinline__ ScanFrame scan_frame(FrameObs v) {
     return f;
 }
 
+// One listed in-window ray: its range (bits) and ray index.
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ bool in_window(float range) {
+    return (int)(range > 0.35f) & (int)(range < 11.5f);
+}
+
+// in_window as one unsigned compare of the bits: 0x3eb33334 is the least
+// float above 0.35f and 0x41380000 is 11.5f; negative values, zeros, NaN
+// and infinities all fall outside [0x3eb33334, 0x41380000).
+__device__ __forceinline__ bool in_window_bits(float range) {
+    return __float_as_uint(range) - 0x3eb33334u < 0x41380000u - 0x3eb33334u;
+}
+
+// onboard_features.cuh:199-207 for one ray with rotated direction rw:
+// returns the corridor centre x (+inf when the ray is outside the window or
+// the corridor) and sets y_center.  Bitwise, so the compares stay one
+// straight-line block.
+__device__ __forceinline__ float corridor_centre(float rwx, float rwy, float rwz, float range,
+                                                 float py, float &y_center) {
+    const float wx = rwx * range, wy = rwy * range, wz = rwz * range;
+    const float x_center = wx + rwx * 1.10f;
+    y_center = py + wy + rwy * 1.10f;
+    const bool corridor = (int)in_window(range) & (int)(fabsf(wz) <= 2.1f) &
+                          (int)(x_center >= -0.35f) & (int)(x_center <= 10.5f) &
+                          (int)(fabsf(y_center) <= 3.5f);
+    return corridor ? x_center : __builtin_huge_valf();
+}
+
 // onboard_features.cuh:184-234 for one environment, on one wave (24 rays per
 // lane, no workgroup barrier).
 //   * The reference maps non-finite ranges to 0 / +-1000 first; both fail
 //     the 0.35 < r < 11.5 window, as NaN does, so the raw value is tested.
+//     The reference skips rays outside the window (:193, :218), and so does
+//     the common path here: the in-window rays are listed in the wave's
+//     `list` (ballot + lane prefix count) and passes 1 and 2 run over the
+//     list, 64 rays per instruction.  When more than kListCap rays are in
+//     the window, every slot is swept instead (the same per-ray arithmetic).
 //   * The closest return over elevation rows 0..3 is found in two steps: the
 //     wave's minimum in-window range (as bits: positive floats order like
 //     their bit patterns), then the first slot in ray order and the first
@@ -255,93 +293,167 @@ __device__ __forceinline__ ScanFrame scan_frame(FrameObs v) {
 //     That is the reference's first minimum in scan order.  Lane 0
 //     recomputes the winner's world offset with the reference's expression,
 //     which gives the value pass 1 formed (see the pair identity below).
-//   * Pass 1 is branch-free and keeps each ray's corridor centre (x = +inf
-//     outside the window or the corridor), so pass 2 is a compare-and-add.
-//   * Once pass 1 has consumed the ranges, the registers take the next
-//     environment's (`next`, a 0-byte resource when there is none): they
-//     have the rest of this environment to arrive.
+//   * Pass 1 keeps each ray's corridor centre (x = +inf outside the window or
+//     the corridor), so pass 2 is a compare-and-add.  The reference's
+//     strict-< update over corridor rays is the minimum of their centres.
+//   * Once the ranges are consumed (listed, or swept by pass 1), the
+//     registers take the next environment's (`next`, a 0-byte resource when
+//     there is none): they have the rest of this environment to arrive.
 //   * `f` is wave-uniform.
 __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes &rays,
                                          const ScanFrame &f, __amdgpu_buffer_rsrc_t next,
-                                         int lane, ScanResult &out) {
-    // Closest return.  A slot outside the window counts as 11.5, the
-    // window's exclusive upper bound, so it never wins.
-    constexpr unsigned kWindowTop = 0x41380000u;  // 11.5f
-    unsigned lane_min = kWindowTop;
+                                         int lane, u32x2 *list, ScanResult &out) {
+    // List the in-window rays in slot order while counting them.  Once a
+    // slot's rays would overflow the list, counting stops: n then exceeds
+    // kListCap and the list is not used.
+    int n = 0;
 #pragma unroll
     for (int u = 0; u < kScanRays; ++u) {
-        if ((u / 2) % 6 >= 4) continue;
-        lane_min = min(lane_min, rg[u] > 0.35f ? __float_as_uint(rg[u]) : kWindowTop);
+        const bool in = in_window_bits(rg[u]);
+        const uint64_t m = __builtin_amdgcn_ballot_w64(in);
+        const int next_n = n + (int)__builtin_popcountll(m);
+        if (next_n > kListCap) {
+            n = next_n;
+            break;
+        }
+        if (in) {
+            const unsigned pos = __builtin_amdgcn_mbcnt_hi(
+                (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+            list[n + pos] = u32x2{__float_as_uint(rg[u]), (unsigned)(64 * u + lane)};
+        }
+        n = next_n;
     }
-    const unsigned min_bits = wave_min_u32(lane_min);
+
+    // Closest return: a ray outside the window or on elevation rows 4..5
+    // counts as 11.5, the window's exclusive upper bound, so it never wins.
+    constexpr unsigned kWindowTop = 0x41380000u;  // 11.5f
+    unsigned min_bits;
     int min_ray = -1;
-    if (min_bits != kWindowTop) {
-        // Visiting slots from the last to the first leaves the first slot
-        // (in ray order) that holds the range, at its first lane.
-#pragma unroll
-        for (int u = kScanRays - 1; u >= 0; --u) {
-            if ((u / 2) % 6 >= 4) continue;
-            const uint64_t hit = __builtin_amdgcn_ballot_w64(__float_as_uint(rg[u]) == min_bits);
-            if (hit) min_ray = 64 * u + (int)__builtin_ctzll(hit);
-        }
-    }
-
-    // Pass 1.  The rays of rows el and el + 6 (heads 0 and 1) at the same
-    // azimuth have the same table x, y and the negated z, bit for bit.  With
-    // the reference's order (R0 d.x + R1 d.y) + R2 d.z the head-1 sum is
-    // therefore P - Q where the head-0 sum is P + Q, exactly (a + (-b) and
-    // a - b are the same IEEE operation), so each pair reads one direction
-    // and forms P and Q once.
     float min_dx_c = 30.0f;
-    float xc[kScanRays], yc[kScanRays];
-#pragma unroll
-    for (int el = 0; el < 6; ++el) {
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int ray = 128 * el + 64 * half + lane;
-            const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
-            const float p0 = f.r[0] * dx + f.r[1] * dy, q0 = f.r[2] * dz;
-            const float p1 = f.r[3] * dx + f.r[4] * dy, q1 = f.r[5] * dz;
-            const float p2 = f.r[6] * dx + f.r[7] * dy, q2 = f.r[8] * dz;
-#pragma unroll
-            for (int head = 0; head < 2; ++head) {
-                const int u = 2 * (6 * head + el) + half;
-                const float range = rg[u];
-                const float rwx = head ? p0 - q0 : p0 + q0;
-                const float rwy = head ? p1 - q1 : p1 + q1;
-                const float rwz = head ? p2 - q2 : p2 + q2;
-                const float wx = rwx * range, wy = rwy * range, wz = rwz * range;
-                const float x_center = wx + rwx * 1.10f;
-                const float y_center = f.py + wy + rwy * 1.10f;
-                // Bitwise, so the compares stay one straight-line block.
-                const bool corridor = (int)(range > 0.35f) & (int)(range < 11.5f) &
-                                      (int)(fabsf(wz) <= 2.1f) & (int)(x_center >= -0.35f) &
-                                      (int)(x_center <= 10.5f) & (int)(fabsf(y_center) <= 3.5f);
-                xc[u] = corridor ? x_center : __builtin_huge_valf();
-                yc[u] = y_center;
-                // The reference's strict-< update over corridor rays is the
-                // minimum of their centres (+inf elsewhere): exact.
-                min_dx_c = fminf(min_dx_c, xc[u]);
-            }
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    load_ranges(next, lane, rg);
-    min_dx_c = wave_min(min_dx_c);
-
-    // Pass 2: the cluster is counted from the lane masks (scalar unit); y is
-    // summed in double.  Adding +0.0 for the rays outside the cluster leaves
-    // the sum unchanged: it starts at +0.0 and never becomes -0.0.
-    const float limit = min_dx_c + 1.4f;
     int count = 0;
     double y_sum = 0.0;
+    if (n <= kListCap) {
+        // The list is written and read by this wave only.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        load_ranges(next, lane, rg);
+        float xl[kListRounds], yl[kListRounds];
+        unsigned key[kListRounds];
+        int ray_of[kListRounds];
+        unsigned lane_min = kWindowTop;
 #pragma unroll
-    for (int u = 0; u < kScanRays; ++u) {
-        const bool in = xc[u] <= limit;
-        count += __builtin_popcountll(__builtin_amdgcn_ballot_w64(in));
-        float y = in ? yc[u] : 0.0f;
-        asm("" : "+v"(y));  // select the float, then widen (one select, not two)
-        y_sum += (double)y;
+        for (int r = 0; r < kListRounds; ++r) {
+            xl[r] = __builtin_huge_valf();
+            yl[r] = 0.0f;
+            key[r] = kWindowTop;
+            ray_of[r] = 0;
+            if (64 * r < n) {
+                const int e = 64 * r + lane;
+                const u32x2 entry = list[e];
+                const bool valid = e < n;
+                // Entries past n are left from earlier environments: a range
+                // of 0 fails the window.
+                const float range = valid ? __uint_as_float(entry.x) : 0.0f;
+                const int ray = valid ? (int)entry.y : 0;
+                // Ray 128 row + azimuth, row = 6 head + el: el < 4 on rows
+                // 0..3 and 6..9.
+                const bool low_row = ((0x3cfu >> (ray >> 7)) & 1u) != 0u;
+                key[r] = ((int)valid & (int)low_row) ? entry.x : kWindowTop;
+                ray_of[r] = ray;
+                lane_min = min(lane_min, key[r]);
+                const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
+                const float rwx = f.r[0] * dx + f.r[1] * dy + f.r[2] * dz;
+                const float rwy = f.r[3] * dx + f.r[4] * dy + f.r[5] * dz;
+                const float rwz = f.r[6] * dx + f.r[7] * dy + f.r[8] * dz;
+                xl[r] = corridor_centre(rwx, rwy, rwz, range, f.py, yl[r]);
+                min_dx_c = fminf(min_dx_c, xl[r]);
+            }
+        }
+        min_bits = wave_min_u32(lane_min);
+        if (min_bits != kWindowTop) {
+            // The list runs in ray order, so the first round and lane
+            // holding the minimum is the reference's first minimum.
+#pragma unroll
+            for (int r = 0; r < kListRounds; ++r) {
+                const uint64_t hit = __builtin_amdgcn_ballot_w64(key[r] == min_bits);
+                if (hit) {
+                    min_ray = __builtin_amdgcn_readlane(ray_of[r], (int)__builtin_ctzll(hit));
+                    break;
+                }
+            }
+        }
+        min_dx_c = wave_min(min_dx_c);
+        const float limit = min_dx_c + 1.4f;
+#pragma unroll
+        for (int r = 0; r < kListRounds; ++r) {
+            if (64 * r >= n) break;
+            const bool in = xl[r] <= limit;
+            count += __builtin_popcountll(__builtin_amdgcn_ballot_w64(in));
+            float y = in ? yl[r] : 0.0f;
+            asm("" : "+v"(y));  // select the float, then widen (one select, not two)
+            y_sum += (double)y;
+        }
+    } else {
+        // Every slot.  The rays of rows el and el + 6 (heads 0 and 1) at the
+        // same azimuth have the same table x, y and the negated z, bit for
+        // bit.  With the reference's order (R0 d.x + R1 d.y) + R2 d.z the
+        // head-1 sum is therefore P - Q where the head-0 sum is P + Q,
+        // exactly (a + (-b) and a - b are the same IEEE operation), so each
+        // pair reads one direction and forms P and Q once.
+        unsigned lane_min = kWindowTop;
+#pragma unroll
+        for (int u = 0; u < kScanRays; ++u) {
+            if ((u / 2) % 6 >= 4) continue;
+            lane_min = min(lane_min, rg[u] > 0.35f ? __float_as_uint(rg[u]) : kWindowTop);
+        }
+        min_bits = wave_min_u32(lane_min);
+        if (min_bits != kWindowTop) {
+            // Visiting slots from the last to the first leaves the first slot
+            // (in ray order) that holds the range, at its first lane.
+#pragma unroll
+            for (int u = kScanRays - 1; u >= 0; --u) {
+                if ((u / 2) % 6 >= 4) continue;
+                const uint64_t hit =
+                    __builtin_amdgcn_ballot_w64(__float_as_uint(rg[u]) == min_bits);
+                if (hit) min_ray = 64 * u + (int)__builtin_ctzll(hit);
+            }
+        }
+        float xc[kScanRays], yc[kScanRays];
+#pragma unroll
+        for (int el = 0; el < 6; ++el) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int ray = 128 * el + 64 * half + lane;
+                const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
+                const float p0 = f.r[0] * dx + f.r[1] * dy, q0 = f.r[2] * dz;
+                const float p1 = f.r[3] * dx + f.r[4] * dy, q1 = f.r[5] * dz;
+                const float p2 = f.r[6] * dx + f.r[7] * dy, q2 = f.r[8] * dz;
+#pragma unroll
+                for (int head = 0; head < 2; ++head) {
+                    const int u = 2 * (6 * head + el) + half;
+                    xc[u] = corridor_centre(head ? p0 - q0 : p0 + q0, head ? p1 - q1 : p1 + q1,
+                                            head ? p2 - q2 : p2 + q2, rg[u], f.py, yc[u]);
+                    min_dx_c = fminf(min_dx_c, xc[u]);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_ranges(next, lane, rg);
+        min_dx_c = wave_min(min_dx_c);
+        // Pass 2: the cluster is counted from the lane masks (scalar unit);
+        // y is summed in double.  Adding +0.0 for the rays outside the
+        // cluster leaves the sum unchanged: it starts at +0.0 and never
+        // becomes -0.0.
+        const float limit = min_dx_c + 1.4f;
+#pragma unroll
+        for (int u = 0; u < kScanRays; ++u) {
+            const bool in = xc[u] <= limit;
+            count += __builtin_popcountll(__builtin_amdgcn_ballot_w64(in));
+            float y = in ? yc[u] : 0.0f;
+            asm("" : "+v"(y));  // select the float, then widen (one select, not two)
+            y_sum += (double)y;
+        }
     }
     y_sum = wave_sum_double(y_sum);
     if (lane == 0) {
@@ -989,6 +1101,7 @@ __device__ __forceinline__ void actor_scalars(float raw, int lane, float *propri
 template <bool SCALARS>
 __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows rows) {
     __shared__ RayPlanes rays;
+    __shared__ u32x2 lists[kWavesPerBlock][kListCap];
     const int tid = threadIdx.x, lane = tid & 63;
     for (int i = tid; i < 1536; i += kBlockThreads) {
         rays.d[0][i] = kRayDir[i * 3 + 0];
@@ -1033,7 +1146,7 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
         const bool has_next = next_env < rows.batch;
         ScanResult s;
         scan_env(rg, rays, f, obs_rsrc(has_next ? obs_of(next_env) : nullptr, has_next), lane,
-                 s);
+                 lists[__builtin_amdgcn_readfirstlane(tid >> 6)], s);
         if (lane == 0) {
             float *park = rows.prior + env * 15;
             park[0] = s.min_r;
