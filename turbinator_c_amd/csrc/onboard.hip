@@ -316,11 +316,13 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
             n = next_n;
             break;
         }
-        if (in) {
-            const unsigned pos = __builtin_amdgcn_mbcnt_hi(
-                (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
-            list[n + pos] = u32x2{__float_as_uint(rg[u]), (unsigned)(64 * u + lane)};
-        }
+        // Lanes outside the window write to their own spare entry, so the
+        // store needs no branch.
+        unsigned pos = __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+        asm volatile("" : "+v"(pos));  // formed on every lane, then selected
+        list[in ? n + pos : kListCap + lane] =
+            u32x2{__float_as_uint(rg[u]), (unsigned)(64 * u + lane)};
         n = next_n;
     }
 
@@ -1101,7 +1103,7 @@ __device__ __forceinline__ void actor_scalars(float raw, int lane, float *propri
 template <bool SCALARS>
 __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows rows) {
     __shared__ RayPlanes rays;
-    __shared__ u32x2 lists[kWavesPerBlock][kListCap];
+    __shared__ u32x2 lists[kWavesPerBlock][kListCap + 64];  // + a spare entry per lane
     const int tid = threadIdx.x, lane = tid & 63;
     for (int i = tid; i < 1536; i += kBlockThreads) {
         rays.d[0][i] = kRayDir[i * 3 + 0];
@@ -1173,85 +1175,155 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
     }
 }
 
+// Phase 2's inputs for the 64 environments of a workgroup: obs[0..47],
+// mission[0..9] and the parked scan result.  Odd row pitches put the rows a
+// wave reads (64 lanes, or 16 quads) on different LDS banks.
+constexpr int kStageObs = 48, kStageObsPitch = 49, kStageMissionPitch = 11, kStageScanPitch = 9;
+struct ControlStage {
+    float obs[64][kStageObsPitch];
+    float mission[64][kStageMissionPitch];
+    float scan[64][kStageScanPitch];
+};
+
 // Phase 2: the tactical features and the controller, from the parked scan
 // result.  A 320-thread workgroup covers 64 environments: wave 0 runs the
 // tactical features, one lane per environment; waves 1..4 run the
 // controller, one quad of lanes per environment (16 per wave), lane a of the
 // quad on arm a.  Both are long scalar chains and few waves exist per
 // launch, so splitting the work shortens the chains and spreads them over
-// more SIMDs.  Values are formed in registers and then stored to each
-// destination (the tactical / prior rows and, for the actor, their copies in
-// proprio and mission_vec).
+// more SIMDs.
+//   * The workgroup first stages every input its chains read (all loads
+//     issued at once, coalesced over the rows' first 192 bytes), so the
+//     chains read LDS: read from global memory at their points of use, the
+//     values came in a dozen dependent round trips.
+//   * Values are formed in registers and then stored to each destination
+//     (the tactical / prior rows and, for the actor, their copies in
+//     proprio and mission_vec).
 __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(OnboardRows rows) {
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    __shared__ ControlStage stage;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int slot = w == 0 ? lane : 16 * (w - 1) + (lane >> 2);  // environment within the 64
     const int a = lane & 3;
-    for (size_t env = (size_t)blockIdx.x * 64 + slot; env < rows.batch;
-         env += (size_t)gridDim.x * 64) {
-        const float *obs = reinterpret_cast<const float *>(rows.obs + env * rows.obs_stride);
-        const float *mission =
-            reinterpret_cast<const float *>(rows.mission + env * rows.mission_stride);
-        if (w == 0) {
-            float t[24];
-            tactical_features(obs, mission, t);
-            float *tac = rows.tactical + env * 24;
+    for (size_t base = (size_t)blockIdx.x * 64; base < rows.batch;
+         base += (size_t)gridDim.x * 64) {
+        // Rows past the batch end re-read the last row; nothing uses them.
+        auto row_of = [&](int e) {
+            const size_t env = base + (size_t)e;
+            return env < rows.batch ? env : rows.batch - 1;
+        };
+        constexpr int kObsLoads = (64 * kStageObs + kControlThreads - 1) / kControlThreads;
+        constexpr int kMissionLoads = (64 * 10 + kControlThreads - 1) / kControlThreads;
+        constexpr int kScanLoads = (64 * 7 + kControlThreads - 1) / kControlThreads;
+        // Every thread issues all its loads unconditionally (an index past
+        // the stage re-reads the stage's last value), so they leave at once.
+        float vo[kObsLoads], vm[kMissionLoads], vs[kScanLoads];
 #pragma unroll
-            for (int i = 0; i < 24; ++i) tac[i] = t[i];
-            if (rows.proprio) {
-                float *p = rows.proprio + env * 91, *mv = rows.mission_vec + env * 49;
+        for (int k = 0; k < kObsLoads; ++k) {
+            const int idx = min(tid + kControlThreads * k, 64 * kStageObs - 1);
+            const int e = idx / kStageObs, i = idx - kStageObs * e;
+            vo[k] = reinterpret_cast<const float *>(rows.obs + row_of(e) * rows.obs_stride)[i];
+        }
 #pragma unroll
-                for (int i = 0; i < 24; ++i) {
-                    p[52 + i] = t[i];
-                    mv[10 + i] = t[i];
+        for (int k = 0; k < kMissionLoads; ++k) {
+            const int idx = min(tid + kControlThreads * k, 64 * 10 - 1);
+            const int e = idx / 10, i = idx - 10 * e;
+            vm[k] = reinterpret_cast<const float *>(rows.mission + row_of(e) * rows.mission_stride)[i];
+        }
+#pragma unroll
+        for (int k = 0; k < kScanLoads; ++k) {
+            const int idx = min(tid + kControlThreads * k, 64 * 7 - 1);
+            const int e = idx / 7, i = idx - 7 * e;
+            vs[k] = rows.prior[row_of(e) * 15 + i];
+        }
+#pragma unroll
+        for (int k = 0; k < kObsLoads; ++k) {
+            const int idx = tid + kControlThreads * k;
+            const int e = idx / kStageObs;
+            if (idx < 64 * kStageObs) stage.obs[e][idx - kStageObs * e] = vo[k];
+        }
+#pragma unroll
+        for (int k = 0; k < kMissionLoads; ++k) {
+            const int idx = tid + kControlThreads * k;
+            const int e = idx / 10;
+            if (idx < 64 * 10) stage.mission[e][idx - 10 * e] = vm[k];
+        }
+#pragma unroll
+        for (int k = 0; k < kScanLoads; ++k) {
+            const int idx = tid + kControlThreads * k;
+            const int e = idx / 7;
+            if (idx < 64 * 7) stage.scan[e][idx - 7 * e] = vs[k];
+        }
+        __syncthreads();
+
+        const size_t env = base + (size_t)slot;
+        if (env < rows.batch) {
+            const float *obs = stage.obs[slot];
+            const float *mission = stage.mission[slot];
+            if (w == 0) {
+                float t[24];
+                tactical_features(obs, mission, t);
+                float *tac = rows.tactical + env * 24;
+#pragma unroll
+                for (int i = 0; i < 24; ++i) tac[i] = t[i];
+                if (rows.proprio) {
+                    float *p = rows.proprio + env * 91, *mv = rows.mission_vec + env * 49;
+#pragma unroll
+                    for (int i = 0; i < 24; ++i) {
+                        p[52 + i] = t[i];
+                        mv[10 + i] = t[i];
+                    }
+                }
+            } else {
+                const float *sc = stage.scan[slot];
+                ScanResult s;
+                s.min_r = sc[0];
+                s.min_r_dx = sc[1];
+                s.min_r_dy = sc[2];
+                s.min_dx_c = sc[3];
+                s.cluster_y_sum = sc[4];
+                s.min_ray = __float_as_int(sc[5]);
+                s.cluster_count = __float_as_int(sc[6]);
+                const ArmOutputs n = prior_features(obs, mission, s, a);
+                // The parked result was staged before the chain; each lane
+                // now writes its arm's three values, lane 0 the cannon's.
+                float *prior = rows.prior + env * 15;
+                prior[a] = n.throttle;
+                prior[4 + a] = n.outer;
+                prior[8 + a] = n.inner;
+                if (a == 0) {
+                    prior[12] = n.az;
+                    prior[13] = n.el;
+                    prior[14] = n.fire;
+                }
+                if (rows.proprio) {
+                    float *p = rows.proprio + env * 91 + 76, *mv = rows.mission_vec + env * 49 + 34;
+                    p[a] = n.throttle;
+                    p[4 + a] = n.outer;
+                    p[8 + a] = n.inner;
+                    mv[a] = n.throttle;
+                    mv[4 + a] = n.outer;
+                    mv[8 + a] = n.inner;
+                    if (a == 0) {
+                        p[12] = n.az;
+                        p[13] = n.el;
+                        p[14] = n.fire;
+                        mv[12] = n.az;
+                        mv[13] = n.el;
+                        mv[14] = n.fire;
+                    }
+                }
+                if (rows.diag && a == 0) {
+                    float *d = rows.diag + env * 4;
+                    d[0] = s.min_r;
+                    d[1] = (float)s.min_ray;
+                    d[2] = s.min_dx_c;
+                    d[3] = (float)s.cluster_count;
                 }
             }
-            continue;
         }
-        float *prior = rows.prior + env * 15;
-        ScanResult s;
-        s.min_r = prior[0];
-        s.min_r_dx = prior[1];
-        s.min_r_dy = prior[2];
-        s.min_dx_c = prior[3];
-        s.cluster_y_sum = prior[4];
-        s.min_ray = __float_as_int(prior[5]);
-        s.cluster_count = __float_as_int(prior[6]);
-        const ArmOutputs n = prior_features(obs, mission, s, a);
-        // The parked result was read by all four lanes before the chain;
-        // each lane now writes its arm's three values, lane 0 the cannon's.
-        prior[a] = n.throttle;
-        prior[4 + a] = n.outer;
-        prior[8 + a] = n.inner;
-        if (a == 0) {
-            prior[12] = n.az;
-            prior[13] = n.el;
-            prior[14] = n.fire;
-        }
-        if (rows.proprio) {
-            float *p = rows.proprio + env * 91 + 76, *mv = rows.mission_vec + env * 49 + 34;
-            p[a] = n.throttle;
-            p[4 + a] = n.outer;
-            p[8 + a] = n.inner;
-            mv[a] = n.throttle;
-            mv[4 + a] = n.outer;
-            mv[8 + a] = n.inner;
-            if (a == 0) {
-                p[12] = n.az;
-                p[13] = n.el;
-                p[14] = n.fire;
-                mv[12] = n.az;
-                mv[13] = n.el;
-                mv[14] = n.fire;
-            }
-        }
-        if (rows.diag && a == 0) {
-            float *d = rows.diag + env * 4;
-            d[0] = s.min_r;
-            d[1] = (float)s.min_ray;
-            d[2] = s.min_dx_c;
-            d[3] = (float)s.cluster_count;
-        }
+        // The stage is reused by this workgroup's next 64 environments.
+        if (base + (size_t)gridDim.x * 64 < rows.batch) __syncthreads();
     }
 }
 
