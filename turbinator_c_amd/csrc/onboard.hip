@@ -1054,40 +1054,26 @@ __device__ __forceinline__ float actor_scale(int i) {  // network_gpu.cu:287-293
 // network_gpu.cu:285-297 (scalar_inputs): lanes 0..51 of a wave write the
 // environment's 52 symlog scalars, lanes 52..61 its 10 finite mission values.
 // The input of lane l is obs[l] (l < 48), obs[4144 + l - 48] (l < 52) or
-// mission[l - 52] (l < 62); it is requested one environment ahead, through
-// buffer resources (0 bytes when there is no such environment), so that its
-// round trip overlaps that environment's scan.
-constexpr unsigned kMissionRowBytes = 10 * sizeof(float);
-constexpr int kPastRecords = 0x40000000;  // past every resource: reads 0
+// mission[l - 52] (l < 62).  Branch-free: every lane forms both values, and
+// buffer stores (discarded past num_records) write lanes 0..51 into proprio
+// and 52..61 into mission_vec; an environment that is not `valid` writes
+// nothing.
+constexpr int kPastRecords = 0x40000000;  // past every resource
 
-__device__ __forceinline__ float actor_scalar_input(__amdgpu_buffer_rsrc_t obs,
-                                                    __amdgpu_buffer_rsrc_t mission, int lane) {
-    const int obs_off = lane < 48 ? 4 * lane : (lane < 52 ? 4 * (4096 + lane) : kPastRecords);
-    const int mission_off = lane >= 52 && lane < 62 ? 4 * (lane - 52) : kPastRecords;
-    const float o =
-        __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(obs, obs_off, 0, 0));
-    const float m =
-        __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(mission, mission_off, 0, 0));
-    return lane < 52 ? o : m;
-}
-
-// Branch-free: every lane forms both values, and buffer stores (discarded
-// past num_records) write lanes 0..51 into proprio and 52..61 into
-// mission_vec.  A store issued on one path only would make the compiler
-// wait for every outstanding load (the next ranges) where the paths join.
 __device__ __forceinline__ void actor_scalars(float raw, int lane, float *proprio,
-                                              float *mission_vec) {
+                                              float *mission_vec, bool valid) {
     const bool finite = __builtin_isfinite(raw);
     const float clamped = finite ? fmaxf(-1000.0f, fminf(1000.0f, raw)) : 0.0f;
     const float symlog = copysignf(log1p_pos(fabsf(clamped * actor_scale(lane))), clamped);
     const float scaled = fmaxf(-8.0f, fminf(8.0f, symlog / sqrtf(1.0001f)));
     __builtin_amdgcn_raw_buffer_store_b32(
         __builtin_bit_cast(unsigned, scaled),
-        __builtin_amdgcn_make_buffer_rsrc(proprio, (short)0, 52 * 4, kBufferWord3),
+        __builtin_amdgcn_make_buffer_rsrc(proprio, (short)0, valid ? 52 * 4 : 0, kBufferWord3),
         lane < 52 ? 4 * lane : kPastRecords, 0, 0);
     __builtin_amdgcn_raw_buffer_store_b32(
         __builtin_bit_cast(unsigned, finite ? raw : 0.0f),
-        __builtin_amdgcn_make_buffer_rsrc(mission_vec, (short)0, 10 * 4, kBufferWord3),
+        __builtin_amdgcn_make_buffer_rsrc(mission_vec, (short)0, valid ? 10 * 4 : 0,
+                                          kBufferWord3),
         lane >= 52 && lane < 62 ? 4 * (lane - 52) : kPastRecords, 0, 0);
 }
 
@@ -1101,7 +1087,6 @@ __device__ __forceinline__ void actor_scalars(float raw, int lane, float *propri
 // 32-byte result is parked in the environment's own prior row (60 bytes),
 // which phase 2 reads before it writes the 15 prior values there: no
 // scratch memory is needed.
-template <bool SCALARS>
 __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows rows) {
     __shared__ RayPlanes rays;
     __shared__ u32x2 lists[kWavesPerBlock][kListCap + 64];  // + a spare entry per lane
@@ -1125,17 +1110,8 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
         return load_frame_obs(obs_of(e < rows.batch ? e : first));
     };
     const FrameObs first_obs = frame_obs(env);
-    auto mission_rsrc = [&](size_t e, bool valid) {
-        return __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<unsigned char *>(rows.mission + e * rows.mission_stride), (short)0,
-            valid ? (int)kMissionRowBytes : 0, kBufferWord3);
-    };
     float rg[kScanRays];
     load_ranges(obs_rsrc(obs_of(env), true), lane, rg);
-    float scalar_in = 0.0f;
-    if (SCALARS)
-        scalar_in =
-            actor_scalar_input(obs_rsrc(obs_of(env), true), mission_rsrc(env, true), lane);
     ScanFrame mine = scan_frame(first_obs);
     for (int k = 0;;) {
         ScanFrame f;
@@ -1160,13 +1136,6 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
             park[5] = __int_as_float(s.min_ray);
             park[6] = __int_as_float(s.cluster_count);
         }
-        if (SCALARS) {
-            const float scalar_next = actor_scalar_input(
-                obs_rsrc(has_next ? obs_of(next_env) : nullptr, has_next),
-                mission_rsrc(has_next ? next_env : 0, has_next), lane);
-            actor_scalars(scalar_in, lane, rows.proprio + env * 91, rows.mission_vec + env * 49);
-            scalar_in = scalar_next;
-        }
         if (!has_next) break;
         env = next_env;
         if (++k == 64) {  // the next 64 environments of this wave
@@ -1184,15 +1153,19 @@ struct ControlStage {
     float obs[64][kStageObsPitch];
     float mission[64][kStageMissionPitch];
     float scan[64][kStageScanPitch];
+    float tail[64][5];  // obs[4144..4147], for the actor's scalar wave
 };
 
 // Phase 2: the tactical features and the controller, from the parked scan
-// result.  A 320-thread workgroup covers 64 environments: wave 0 runs the
-// tactical features, one lane per environment; waves 1..4 run the
-// controller, one quad of lanes per environment (16 per wave), lane a of the
-// quad on arm a.  Both are long scalar chains and few waves exist per
-// launch, so splitting the work shortens the chains and spreads them over
-// more SIMDs.
+// result.  A workgroup covers 64 environments: wave 0 runs the tactical
+// features, one lane per environment; waves 1..4 run the controller, one
+// quad of lanes per environment (16 per wave), lane a of the quad on arm a.
+// Both are long scalar chains and few waves exist per launch, so splitting
+// the work shortens the chains and spreads them over more SIMDs.  For the
+// actor's inputs (SCALARS) each controller wave then writes the symlog
+// scalars and mission values of its 16 environments, one environment per
+// step (on the scan waves they cost the scan kernel 6 µs and the following
+// plane kernel 6 µs more; here they add 3 µs to this kernel).
 //   * The workgroup first stages every input its chains read (all loads
 //     issued at once, coalesced over the rows' first 192 bytes), so the
 //     chains read LDS: read from global memory at their points of use, the
@@ -1200,6 +1173,7 @@ struct ControlStage {
 //   * Values are formed in registers and then stored to each destination
 //     (the tactical / prior rows and, for the actor, their copies in
 //     proprio and mission_vec).
+template <bool SCALARS>
 __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(OnboardRows rows) {
     __shared__ ControlStage stage;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1218,7 +1192,7 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
         constexpr int kScanLoads = (64 * 7 + kControlThreads - 1) / kControlThreads;
         // Every thread issues all its loads unconditionally (an index past
         // the stage re-reads the stage's last value), so they leave at once.
-        float vo[kObsLoads], vm[kMissionLoads], vs[kScanLoads];
+        float vo[kObsLoads], vm[kMissionLoads], vs[kScanLoads], vt = 0.0f;
 #pragma unroll
         for (int k = 0; k < kObsLoads; ++k) {
             const int idx = min(tid + kControlThreads * k, 64 * kStageObs - 1);
@@ -1236,6 +1210,12 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
             const int idx = min(tid + kControlThreads * k, 64 * 7 - 1);
             const int e = idx / 7, i = idx - 7 * e;
             vs[k] = rows.prior[row_of(e) * 15 + i];
+        }
+        if (SCALARS) {
+            const int idx = min(tid, 64 * 4 - 1);
+            const int e = idx / 4;
+            vt = reinterpret_cast<const float *>(
+                rows.obs + row_of(e) * rows.obs_stride)[4144 + idx - 4 * e];
         }
 #pragma unroll
         for (int k = 0; k < kObsLoads; ++k) {
@@ -1255,6 +1235,7 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
             const int e = idx / 7;
             if (idx < 64 * 7) stage.scan[e][idx - 7 * e] = vs[k];
         }
+        if (SCALARS && tid < 64 * 4) stage.tail[tid / 4][tid % 4] = vt;
         __syncthreads();
 
         const size_t env = base + (size_t)slot;
@@ -1323,6 +1304,24 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
                 }
             }
         }
+        if (SCALARS && w > 0) {
+            // Lane l's input: obs[l] (l < 48), obs[4144 + l - 48] (l < 52),
+            // mission[l - 52] (l < 62).
+            const int lo = min(lane, kStageObs - 1), lt = min(max(lane - 48, 0), 3),
+                      lm = min(max(lane - 52, 0), 9);
+            // Rows past the batch end (staged as copies of the last row)
+            // store nothing.
+#pragma unroll 4
+            for (int e = 16 * (w - 1); e < 16 * w; ++e) {
+                const float raw = lane < 48 ? stage.obs[e][lo]
+                                            : (lane < 52 ? stage.tail[e][lt] : stage.mission[e][lm]);
+                const size_t env = base + (size_t)e;
+                const bool valid = env < rows.batch;
+                const size_t row = valid ? env : base;
+                actor_scalars(raw, lane, rows.proprio + row * 91, rows.mission_vec + row * 49, valid);
+            }
+        }
+
         // The stage is reused by this workgroup's next 64 environments.
         if (base + (size_t)gridDim.x * 64 < rows.batch) __syncthreads();
     }
@@ -1332,12 +1331,12 @@ int launch_onboard(const OnboardRows &rows, hipStream_t s) {
     const size_t scan_want = (rows.batch + kWavesPerBlock - 1) / kWavesPerBlock;
     const unsigned scan_blocks = scan_want > kScanBlocks ? kScanBlocks : (unsigned)scan_want;
     const size_t ctrl_want = (rows.batch + 63) / 64;
+    onboard_scan_kernel<<<scan_blocks, kBlockThreads, 0, s>>>(rows);
+    const unsigned ctrl_blocks = ctrl_want > kControlBlocks ? kControlBlocks : (unsigned)ctrl_want;
     if (rows.proprio)
-        onboard_scan_kernel<true><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
+        onboard_control_kernel<true><<<ctrl_blocks, kControlThreads, 0, s>>>(rows);
     else
-        onboard_scan_kernel<false><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
-    onboard_control_kernel<<<ctrl_want > kControlBlocks ? kControlBlocks : (unsigned)ctrl_want,
-                             kControlThreads, 0, s>>>(rows);
+        onboard_control_kernel<false><<<ctrl_blocks, kControlThreads, 0, s>>>(rows);
     return hipGetLastError() == hipSuccess;
 }
 
