@@ -157,10 +157,11 @@ def test_config_16384(torch_cuda, hip):
 
 def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
     """As for the onboard entry: 263,144 rows tiled from 4,096 distinct
-    environments (the scan waves form a second group of 64 frames and carry
-    the symlog inputs one environment ahead across it); proprio, mission,
-    tactical and prior rows must equal the 4,096-row call's bit for bit.
-    The plane outputs are left out (they do not depend on the scan)."""
+    environments (the scan waves form a second group of 64 frames, and the
+    control kernel's workgroups, which also write the symlog scalars, loop
+    past their 4,096-workgroup cap); proprio, mission, tactical and prior
+    rows must equal the 4,096-row call's bit for bit.  The plane outputs are
+    left out (they do not depend on the scan)."""
     torch = torch_cuda
     distinct, batch = 4096, 64 * 4096 + 1000
     note(f"actor inputs {batch} envs tiled from {distinct}")
