@@ -1,25 +1,29 @@
-/* Exhaustive check that the depth camera kernel's quotient
- *   q = (float)((double)x * RN_double(1/200))
- * equals the IEEE single-precision quotient x / 200.0f for every float x in
- * [0, 200] (and -0.0).  Why it can hold: x/200 = (x/8)/25 and 1/25 has a
- * binary period of 20, so a non-representable quotient never lies within
- * ~2^-45 (relative) of a float rounding midpoint, while the double product
- * is within ~2^-52 of the exact quotient.  Prints the mismatch count; exits
- * non-zero on any mismatch. */
+/* Exhaustive checks that a quotient by a constant formed as one double
+ * product equals the IEEE single-precision quotient over the inputs a
+ * kernel gives it:
+ *   - the depth camera map:  (float)((double)x * RN_double(1/200)) == x / 200.0f
+ *     for every float x in [0, 200] (and -0.0).  Why it can hold: x/200 =
+ *     (x/8)/25 and 1/25 has a binary period of 20, so a non-representable
+ *     quotient never lies within ~2^-45 (relative) of a float rounding
+ *     midpoint, while the double product is within ~2^-52 of the exact
+ *     quotient;
+ *   - the actor's symlog scaling: (float)((double)x * RN_double(1/c)) == x / c
+ *     with c = sqrtf(1.0001f), for every float x in [0, 8] (|symlog| is at
+ *     most log1p(1000) < 7; rounding to nearest is symmetric in the sign).
+ * Prints one "<n> values, <m> mismatches" line per check; exits non-zero on
+ * any mismatch. */
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
-int main(void) {
-    const double inv = 1.0 / 200.0;
-    const uint32_t top = 0x43480000u; /* 200.0f */
+static unsigned long long check(float c, double inv, uint32_t top, const char *name) {
     unsigned long long bad = 0, n = 0;
     for (uint32_t bits = 0; bits <= top; ++bits) {
         float x;
         memcpy(&x, &bits, 4);
         const volatile float xv = x;
-        const float want = xv / 200.0f;
+        const float want = xv / c;
         const float got = (float)((double)xv * inv);
         uint32_t a, b;
         memcpy(&a, &want, 4);
@@ -28,7 +32,15 @@ int main(void) {
         ++n;
     }
     const float nz = -0.0f;
-    bad += signbit((float)((double)nz * inv)) != signbit(nz / 200.0f);
-    printf("%llu values, %llu mismatches\n", n, bad);
+    bad += signbit((float)((double)nz * inv)) != signbit(nz / c);
+    printf("%s: %llu values, %llu mismatches\n", name, n, bad);
+    return bad;
+}
+
+int main(void) {
+    const volatile float c_sym = 1.0001f;
+    const float c = sqrtf(c_sym);
+    unsigned long long bad = check(200.0f, 1.0 / 200.0, 0x43480000u /* 200.0f */, "x / 200");
+    bad += check(c, 1.0 / (double)c, 0x41000000u /* 8.0f */, "x / sqrtf(1.0001f)");
     return bad != 0;
 }

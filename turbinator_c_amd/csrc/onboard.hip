@@ -1059,13 +1059,17 @@ __device__ __forceinline__ float actor_scale(int i) {  // network_gpu.cu:287-293
 // and 52..61 into mission_vec; an environment that is not `valid` writes
 // nothing.
 constexpr int kPastRecords = 0x40000000;  // past every resource
+// RN_double(1 / sqrtf(1.0001f)): (float)((double)x * this) equals the IEEE
+// quotient x / sqrtf(1.0001f) for every float |x| <= 8 (checked
+// exhaustively by tests/csrc/check_div_by_constant.c), and |symlog| < 7.
+constexpr double kInvSqrt10001 = 0x1.fff974156e01ep-1;
 
 __device__ __forceinline__ void actor_scalars(float raw, int lane, float *proprio,
                                               float *mission_vec, bool valid) {
     const bool finite = __builtin_isfinite(raw);
     const float clamped = finite ? fmaxf(-1000.0f, fminf(1000.0f, raw)) : 0.0f;
     const float symlog = copysignf(log1p_pos(fabsf(clamped * actor_scale(lane))), clamped);
-    const float scaled = fmaxf(-8.0f, fminf(8.0f, symlog / sqrtf(1.0001f)));
+    const float scaled = fmaxf(-8.0f, fminf(8.0f, (float)((double)symlog * kInvSqrt10001)));
     __builtin_amdgcn_raw_buffer_store_b32(
         __builtin_bit_cast(unsigned, scaled),
         __builtin_amdgcn_make_buffer_rsrc(proprio, (short)0, valid ? 52 * 4 : 0, kBufferWord3),
@@ -1309,16 +1313,23 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
             // mission[l - 52] (l < 62).
             const int lo = min(lane, kStageObs - 1), lt = min(max(lane - 48, 0), 3),
                       lm = min(max(lane - 52, 0), 9);
-            // Rows past the batch end (staged as copies of the last row)
-            // store nothing.
-#pragma unroll 4
-            for (int e = 16 * (w - 1); e < 16 * w; ++e) {
-                const float raw = lane < 48 ? stage.obs[e][lo]
-                                            : (lane < 52 ? stage.tail[e][lt] : stage.mission[e][lm]);
-                const size_t env = base + (size_t)e;
+            // All 16 inputs are read first, so the 16 chains are
+            // independent; rows past the batch end (staged as copies of the
+            // last row) store nothing.
+            float raw[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int e = 16 * (w - 1) + j;
+                raw[j] = lane < 48 ? stage.obs[e][lo]
+                                   : (lane < 52 ? stage.tail[e][lt] : stage.mission[e][lm]);
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const size_t env = base + (size_t)(16 * (w - 1) + j);
                 const bool valid = env < rows.batch;
                 const size_t row = valid ? env : base;
-                actor_scalars(raw, lane, rows.proprio + row * 91, rows.mission_vec + row * 49, valid);
+                actor_scalars(raw[j], lane, rows.proprio + row * 91, rows.mission_vec + row * 49,
+                              valid);
             }
         }
 
