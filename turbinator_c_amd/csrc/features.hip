@@ -29,6 +29,7 @@
 
 #include "turbinator/training/cuda_features.h"
 #include "turbinator/training/hip_features.h"
+#include "xcd_order.h"
 
 namespace {
 
@@ -228,16 +229,6 @@ __device__ __forceinline__ unsigned min_same_qx(unsigned v) {
     v = min(v, __shfl_xor(v, 16));
     v = min(v, __shfl_xor(v, 32));
     return v;
-}
-
-// Workgroups are dispatched to the 8 XCDs round-robin by id, and each XCD has
-// its own L2.  This bijection of [0, g) gives XCD x the contiguous
-// environments [x n8, (x+1) n8) (n8 = g / 8; ids past 8 n8 map to
-// themselves), so neighbouring environments, whose rows share cache lines at
-// their ends, meet in the same L2.
-__device__ __forceinline__ size_t xcd_contiguous(size_t b, size_t g) {
-    const size_t n8 = g / 8;
-    return b < 8 * n8 ? (b % 8) * n8 + b / 8 : b;
 }
 
 // LV: floats per LiDAR load (4, 2 or 1 from the row alignment).

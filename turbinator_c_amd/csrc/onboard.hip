@@ -35,6 +35,7 @@
 #include <type_traits>
 
 #include "turbinator/training/hip_features.h"
+#include "xcd_order.h"
 
 #include "onboard_rays.inc"
 
@@ -1411,15 +1412,6 @@ __device__ __forceinline__ f32x4 lidar_channel4(f32x4 r, int kind) {
                          : (kind == 1 ? (valid ? clamped / 30.0f : 1.0f) : (valid ? 1.0f : 0.0f));
     }
     return o;
-}
-
-// Workgroups are dispatched to the 8 XCDs round-robin by id, and each XCD has
-// its own L2.  This bijection of [0, g) gives XCD x the contiguous
-// environments [x n8, (x+1) n8) (n8 = g / 8; ids past 8 n8 map to
-// themselves), so each XCD writes contiguous output.
-__device__ __forceinline__ size_t xcd_contiguous(size_t b, size_t g) {
-    const size_t n8 = g / 8;
-    return b < 8 * n8 ? (b % 8) * n8 + b / 8 : b;
 }
 
 // One 1,024-thread workgroup per environment: thread t loads LiDAR float4 t
