@@ -1394,6 +1394,8 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
+constexpr int kStoreSc1 = 16;  // buffer cache-policy bit 4 (sc1)
+
 struct ActorRows {
     const float *obs;
     const unsigned char *cameras;
@@ -1421,6 +1423,16 @@ __device__ __forceinline__ f32x4 lidar_channel4(f32x4 r, int kind) {
 // XCD-contiguous environment order a pure fill of this pattern reaches
 // 6.3 TB/s on MI355X, against 5.5 TB/s for 256-thread workgroups in
 // dispatch order.
+// One 16-byte store into an environment's output block (`bytes` long) with
+// cache policy sc1.  On MI355X this makes the plane kernel 5% faster than
+// default-policy stores (417 against 440 µs at 16,384 environments).
+__device__ __forceinline__ void store_sc1(float *block, unsigned bytes, unsigned index, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(
+        __builtin_bit_cast(u32x4, v),
+        __builtin_amdgcn_make_buffer_rsrc(block, (short)0, (int)bytes, 0x00020000), index * 16u,
+        0, kStoreSc1);
+}
+
 __global__ __launch_bounds__(kStreamThreads) void actor_stream_kernel(ActorRows rows) {
     const int t = threadIdx.x;
     for (size_t env = xcd_contiguous(blockIdx.x, gridDim.x); env < rows.batch;
@@ -1438,14 +1450,14 @@ __global__ __launch_bounds__(kStreamThreads) void actor_stream_kernel(ActorRows 
         if (rows.lidar) {
             // float4 t is bins 4(t%512).. of head t/512; head h feeds
             // channels h, h+2, h+4.
-            f32x4 *dst = reinterpret_cast<f32x4 *>(rows.lidar + env * 12288);
+            float *dst = rows.lidar + env * 12288;
             const int head = t >> 9, q = t & 511;
 #pragma unroll
             for (int kind = 0; kind < 3; ++kind)
-                dst[(head + 2 * kind) * 512 + q] = lidar_channel4(v, kind);
+                store_sc1(dst, 12288 * 4, (head + 2 * kind) * 512 + q, lidar_channel4(v, kind));
         }
         if (rows.luma) {
-            f32x4 *dst = reinterpret_cast<f32x4 *>(rows.luma + env * 16384);
+            float *dst = rows.luma + env * 16384;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const unsigned w = px[k];
@@ -1453,7 +1465,7 @@ __global__ __launch_bounds__(kStreamThreads) void actor_stream_kernel(ActorRows 
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     o[e] = __builtin_fmaf((float)((w >> (8 * e)) & 0xffu), 1.0f / 255.0f, -0.5f);
-                dst[t + 1024 * k] = o;
+                store_sc1(dst, 16384 * 4, t + 1024 * k, o);
             }
         }
     }
