@@ -64,6 +64,15 @@ struct ScanResult {
     int min_ray, cluster_count, pad;
 };
 
+// x / c for a constant float c, as one double product.  For each constant
+// this file divides by (10, 20, 30, 45, pi/6, pi/4 and the thrust span) the
+// result equals the IEEE quotient for every finite float x
+// (tests/csrc/check_div_by_constant.c, run over all 4.28e9 finite floats);
+// the IEEE division is a ten-instruction dependent sequence.
+__device__ __forceinline__ float div_const(float x, float c) {
+    return (float)((double)x * (1.0 / (double)c));
+}
+
 // onboard_features.cuh:6-22
 __device__ __forceinline__ float ob_clamp(float x, float lo, float hi) {
     if (__builtin_isnan(x)) return x;
@@ -526,7 +535,7 @@ __device__ void tactical_features(const float *o, const float *m, float *t) {
     v[17] = tanhf((-sy * o[3] + cy * o[4]) * 0.15f);
     v[18] = expf(-fmaxf(o[2] - 0.62f, 0.0f));
     const float dist = fmaxf(ob_norm3(rx, ry, rz), 1.0f);
-    const float flight = dist / 20.0f;
+    const float flight = div_const(dist, 20.0f);
     const float wx = rx - o[3] * 0.5f * flight;
     const float wy = ry - o[4] * 0.5f * flight;
     const float wz = rz - o[5] * 0.5f * flight + 0.5f * 9.80665f * flight * flight;
@@ -540,8 +549,8 @@ __device__ void tactical_features(const float *o, const float *m, float *t) {
     const float az = ob_clamp(atan2f(by, bx), pi / 12.0f, pi * 5.0f / 12.0f);
     const float el = ob_clamp(atan2f(bz, fmaxf(hypotf(bx, by), 0.2f)), -pi / 6.0f, pi / 6.0f);
     const float err = hypotf(az - o[44], el - o[45]);
-    v[19] = (az - pi * 0.25f) / (pi / 6.0f);
-    v[20] = el / (pi / 6.0f);
+    v[19] = div_const(az - pi * 0.25f, pi / 6.0f);
+    v[20] = div_const(el, pi / 6.0f);
     v[21] = tanhf(err * 2.0f);
     v[22] = (o[46] <= 0.02f && o[47] > 0.01f && err < 0.26f && dist < 34.0f) ? 1.0f : -1.0f;
     v[23] = sinf(atan2f(ry, rx) - pi * 0.25f - yaw);
@@ -689,7 +698,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     const float scale = fminf(16.0f / fmaxf(hypotf(ax, ay), 1.0e-3f), 1.0f);
     ax *= scale;
     ay *= scale;
-    const float pull = ob_clamp((hypotf(px, py) - 21.0f) / 10.0f, 0.0f, 1.0f);
+    const float pull = ob_clamp(div_const(hypotf(px, py) - 21.0f, 10.0f), 0.0f, 1.0f);
     ax *= 1.0f - pull;
     ay *= 1.0f - pull;
     const float az_t = pz < 8.0f || vz < -1.0f ? 12.2f : ob_clamp(tz, 8.5f, 12.2f);
@@ -701,7 +710,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     // angles join the quad's next atan2 round).
     const float to_x = tx - px, to_y = ty - py, to_z = tz - pz;
     const float dist = fmaxf(ob_norm3(to_x, to_y, to_z), 1.0f);
-    const float flight = dist / 20.0f;
+    const float flight = div_const(dist, 20.0f);
     const float aim_x = to_x - vx * (0.65f * flight);
     const float aim_y = to_y - vy * (0.65f * flight);
     const float aim_z = to_z - vz * (0.65f * flight) + 0.53f * gravity * flight * flight;
@@ -721,7 +730,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
 
     // Sine and cosine of yaw, of the closest return's bearing, of the BWB
     // roll, and of the slalom hill phase.
-    const float hill = ob_clamp((px - 6.0f) / 30.0f, 0.0f, 1.0f);
+    const float hill = ob_clamp(div_const(px - 6.0f, 30.0f), 0.0f, 1.0f);
     const SinCos sc = sin_cos(quad_pick(a, yaw, min_az, roll_right, pi * hill));
     const Quad4 sines = quad_all(sc.s), cosines = quad_all(sc.c);
     const float cyaw = cosines.v[0], syaw = sines.v[0];
@@ -867,7 +876,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
         bty = py + bry;
         float btz = pz + brz;
         const float rxy = hypotf(px, py);
-        const float pull_b = ob_clamp((rxy - 235.0f) / 45.0f, 0.0f, 0.85f);
+        const float pull_b = ob_clamp(div_const(rxy - 235.0f, 45.0f), 0.0f, 0.85f);
         if (arena && rxy > 235.0f) { btx *= 1.0f - pull_b; bty *= 1.0f - pull_b; }
         if (arena) btz = ob_clamp(btz, 28.0f, 135.0f);
         const float gx = btx - px, gy = bty - py;
@@ -938,7 +947,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     float target_thrust = fmaxf(fz_cmd, 0.0f) / nominal_cos;
     if (land_idle) target_thrust = 0.15f * weight * 0.25f;
     const float u_des =
-        ob_clamp((target_thrust - min_thrust) / (max_installed - min_thrust), 0.0f, 1.0f);
+        ob_clamp(div_const(target_thrust - min_thrust, max_installed - min_thrust), 0.0f, 1.0f);
     const float u_raw = u_des + spool_gain * (u_des - spool);
     // The reference's running maximum over arms 0..3, from -inf.
     const Quad4 u_all = quad_all(u_raw);
@@ -963,9 +972,9 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
                       dist < 34.0f;
     const bool cannon = arena && !inv_mode;
     float norm_az =
-        cannon ? ob_clamp((des_cannon_az - cannon_az_ctr) / cannon_az_half, -1.0f, 1.0f) : 0.0f;
+        cannon ? ob_clamp(div_const(des_cannon_az - cannon_az_ctr, cannon_az_half), -1.0f, 1.0f) : 0.0f;
     if (inv_mode) norm_az = -1.0f;
-    float norm_el = cannon ? ob_clamp(des_cannon_el / cannon_el_lim, -1.0f, 1.0f) : 0.0f;
+    float norm_el = cannon ? ob_clamp(div_const(des_cannon_el, cannon_el_lim), -1.0f, 1.0f) : 0.0f;
     float norm_fire = fire ? 0.8f : -0.8f;
 
     if (bwb) {
@@ -1003,14 +1012,14 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
         const float b_err = hypotf(wraps.v[3], b_el - o[45]);
         const bool b_fire = arena && o[46] <= 0.02f && o[47] > 0.01f && b_err < 0.045f &&
                             bdist < 165.0f && bbx > 0.0f;
-        norm_az = arena ? ob_clamp(b_az / (pi / 6.0f), -1.0f, 1.0f) : 0.0f;
-        norm_el = arena ? ob_clamp(b_el / cannon_el_lim, -1.0f, 1.0f) : 0.0f;
+        norm_az = arena ? ob_clamp(div_const(b_az, pi / 6.0f), -1.0f, 1.0f) : 0.0f;
+        norm_el = arena ? ob_clamp(div_const(b_el, cannon_el_lim), -1.0f, 1.0f) : 0.0f;
         norm_fire = b_fire ? 0.8f : -0.8f;
     }
     ArmOutputs out;
     out.throttle = ob_clamp(throttle * 2.0f - 1.0f, -1.0f, 1.0f);
     out.outer = ob_clamp(outer_cmd / outer_limit, -1.0f, 1.0f);
-    out.inner = ob_clamp(inner_cmd / inner_limit, -1.0f, 1.0f);
+    out.inner = ob_clamp(div_const(inner_cmd, inner_limit), -1.0f, 1.0f);
     out.az = norm_az;
     out.el = norm_el;
     out.fire = norm_fire;
@@ -1411,7 +1420,7 @@ __device__ __forceinline__ f32x4 lidar_channel4(f32x4 r, int kind) {
         const bool valid = range > 0.0f && __builtin_isfinite(range);
         const float clamped = fmaxf(0.05f, fminf(30.0f, range));
         o[e] = kind == 0 ? (valid ? 1.0f / fmaxf(0.2f, clamped) : 0.0f)
-                         : (kind == 1 ? (valid ? clamped / 30.0f : 1.0f) : (valid ? 1.0f : 0.0f));
+                         : (kind == 1 ? (valid ? div_const(clamped, 30.0f) : 1.0f) : (valid ? 1.0f : 0.0f));
     }
     return o;
 }
