@@ -1177,9 +1177,9 @@ struct ControlStage {
 // Both are long scalar chains and few waves exist per launch, so splitting
 // the work shortens the chains and spreads them over more SIMDs.  For the
 // actor's inputs (SCALARS) each controller wave then writes the symlog
-// scalars and mission values of its 16 environments, one environment per
-// step (on the scan waves they cost the scan kernel 6 µs and the following
-// plane kernel 6 µs more; here they add 3 µs to this kernel).
+// scalars and mission values of its 16 environments, one row per store (on
+// the scan waves they cost the scan kernel 6 µs and the plane kernel of the
+// next call 6 µs more; here they add about 5 µs to this kernel).
 //   * The workgroup first stages every input its chains read (all loads
 //     issued at once, coalesced over the rows' first 192 bytes), so the
 //     chains read LDS: read from global memory at their points of use, the
