@@ -24,7 +24,7 @@ enum {
     TB_HIP_DIAG_WORDS = 224,
     TB_HIP_TACTICAL_DIM = 24,
     TB_HIP_PRIOR_DIM = 15,
-    TB_HIP_ONBOARD_DIAG_DIM = 4
+    TB_HIP_ONBOARD_DIAG_DIM = 5
 };
 
 /* The 142 features of tb_cuda_extract_features_device (reference
@@ -103,11 +103,12 @@ int tb_hip_lidar_transform_device(const float *ranges, float *out,
  * reference: it runs inside the actor input kernel
  * (src/network/network_gpu.cu:274-304).  Device pointers: obs [batch,4148],
  * mission [batch,10] -> tactical [batch,24], prior [batch,15].  `diag`
- * (nullable, [batch,4]) receives the LiDAR scan results the prior uses:
+ * (nullable, [batch,5]) receives the LiDAR scan results the prior uses:
  * closest in-window return of elevations 0..3, its ray index
- * head*768 + el*128 + azi (-1 if none, as float), the corridor minimum and
- * the cluster count (as float).  Returns 0 for NULL obs/mission/tactical/
- * prior or batch 0 / above 0x7fffffff. */
+ * head*768 + el*128 + azi (-1 if none, as float), the corridor minimum, the
+ * cluster count (as float) and the cluster's y sum, accumulated in float in
+ * the reference's scan order (onboard_features.cuh:231-234).  Returns 0 for
+ * NULL obs/mission/tactical/prior or batch 0 / above 0x7fffffff. */
 int tb_hip_onboard_tactical_prior_device(const float *obs, const float *mission,
                                          float *tactical, float *prior, float *diag,
                                          size_t batch_size, void *stream);

@@ -18,6 +18,8 @@ LIB_ORACLE = HERE / "liboracle.so"
 LIB_REF = HERE / "_ref" / "libref_training.so"
 
 OBS, MISSION, CAMERA, FEATURES, DIAG_WORDS = 4148, 10, 16384, 142, 224
+# min_r, argmin ray, min_dx_c, cluster_count, cluster_y_sum
+ONBOARD_DIAG = 5
 
 _orc = None
 _ref = None
@@ -133,11 +135,11 @@ def lidar_feature(values: np.ndarray, threads: int = 8) -> np.ndarray:
 
 
 def onboard(obs: np.ndarray, mission: np.ndarray):
-    """(tactical [B,24], prior [B,15], diag [B,4]) per environment."""
+    """(tactical [B,24], prior [B,15], diag [B,ONBOARD_DIAG]) per environment."""
     b = obs.shape[0]
     tac = np.empty((b, 24), np.float32)
     pri = np.empty((b, 15), np.float32)
-    diag = np.empty((b, 4), np.float32)
+    diag = np.empty((b, ONBOARD_DIAG), np.float32)
     for e in range(b):
         lib().orc_onboard_env(np.ascontiguousarray(obs[e], np.float32).ctypes.data,
                               np.ascontiguousarray(mission[e], np.float32).ctypes.data,

@@ -14,6 +14,7 @@
  *   diag[1] argmin ray     its ray index (head*768 + el*128 + azi), -1 if none
  *   diag[2] min_dx_c       nearest corridor x-centre (30 when none)
  *   diag[3] cluster_count  rays within 1.4 m of that corridor minimum
+ *   diag[4] cluster_y_sum  their y centres summed in float in scan order
  */
 #include "oracle.h"
 
@@ -306,6 +307,7 @@ static void ob_prior(const float *input_obs, const float *input_mission, float n
         diag[1] = (float)scan.min_ray;
         diag[2] = scan.min_dx_c;
         diag[3] = (float)scan.cluster_count;
+        diag[4] = scan.cluster_y_sum;
     }
 
     const float upx = ex - px, upy = ey - py, upz = ez - pz;
@@ -593,7 +595,7 @@ static void ob_prior(const float *input_obs, const float *input_mission, float n
 
 /* onboard_features.cuh:515-519 */
 void orc_onboard_env(const float *obs, const float *mission,
-                     float *tactical24, float *prior15, float *diag4) {
+                     float *tactical24, float *prior15, float *diag5) {
     ob_tactical(obs, mission, tactical24);
-    ob_prior(obs, mission, prior15, diag4);
+    ob_prior(obs, mission, prior15, diag5);
 }

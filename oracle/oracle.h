@@ -54,9 +54,10 @@ void orc_diagnostics_env(const float *obs, const uint8_t *cameras, uint32_t *dia
 
 /* Onboard tactical (24) and prior (15) features, reference
  * src/network/onboard_features.cuh:25-519.  `diag` (nullable) receives
- * {min_r, argmin ray (as float), min_dx_c, cluster_count (as float)}. */
+ * {min_r, argmin ray (as float), min_dx_c, cluster_count (as float),
+ * cluster_y_sum}. */
 void orc_onboard_env(const float *obs, const float *mission,
-                     float *tactical24, float *prior15, float *diag4);
+                     float *tactical24, float *prior15, float *diag5);
 
 /* The 618M actor's sensor preparation (network_gpu.cu:274-304,467-483):
  * proprio[91], mission_vec[49], tactical[24], prior[15], lidar[6*2048]

@@ -3,8 +3,8 @@ C-ABI entry tb_hip_onboard_tactical_prior_device, against the CPU oracle and
 the reference's own 40 goldens (tests/test_onboard_features.cu:55-85).
 
 Classes: the scan results (closest return, its ray, corridor minimum, cluster
-count) are bit-exact; tactical and prior values within 5e-5 absolute (the
-reference test's tolerance), prior values inside [-1, 1].
+count, cluster y sum) are bit-exact; tactical and prior values within 5e-5
+absolute (the reference test's tolerance), prior values inside [-1, 1].
 """
 from __future__ import annotations
 
@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.test_onboard_oracle import GOLDEN, reference_rows
+from tests.test_onboard_oracle import GOLDEN, near_cancel_rows, reference_rows
 from turbinator_c_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -32,7 +32,7 @@ def run_onboard(torch, hip, obs, mission, with_diag=True):
     d_mis = torch.from_numpy(np.ascontiguousarray(mission)).cuda()
     tac = torch.full((b, 24), float("nan"), dtype=torch.float32, device="cuda")
     pri = torch.full((b, 15), float("nan"), dtype=torch.float32, device="cuda")
-    diag = torch.full((b, 4), float("nan"), dtype=torch.float32, device="cuda") \
+    diag = torch.full((b, oracle.ONBOARD_DIAG), float("nan"), dtype=torch.float32, device="cuda") \
         if with_diag else None
     s = torch.cuda.current_stream()
     torch.cuda.synchronize()
@@ -109,7 +109,7 @@ def scan_ray_columns():
                                     (255, 256, 257, 300, 640, 1000, 1535, 1536)])
 def test_listed_and_swept_scans(torch_cuda, hip, counts):
     """Exactly k of an environment's 1,536 scan rays inside the 0.35..11.5 m
-    window, at random positions: up to 256 the wave lists the in-window rays
+    window, at random positions: up to 512 the wave lists the in-window rays
     and runs the passes over the list, above that it sweeps every slot.  The
     other rays take values just outside the window or non-finite ones."""
     note(f"onboard scans with k in-window rays, k in {counts}")
@@ -142,6 +142,20 @@ def test_listed_and_swept_scans(torch_cuda, hip, counts):
     note(f"counts {counts}: {stats}")
 
 
+@pytest.mark.parametrize("sweep", [False, True])
+def test_near_cancelling_cluster_sign(torch_cuda, hip, sweep):
+    """Slalom clusters whose y centres nearly cancel: the float sum in scan
+    order and the exact sum have opposite signs, and the sign picks the lane
+    target (onboard_features.cuh:238, +-1.85 m).  The cluster y sum must be
+    bit-exact and the prior within tolerance, on the listed pass and (with
+    588 extra in-window rays outside the corridor) on the swept pass."""
+    note(f"onboard near-cancelling clusters, sweep={sweep}")
+    obs, mission = near_cancel_rows(sweep)
+    got = run_onboard(torch_cuda, hip, obs, mission)
+    stats = compare(got, oracle.onboard(obs, mission), f"near-cancel sweep={sweep}")
+    note(f"near-cancel sweep={sweep}: {stats}")
+
+
 def test_benchmark_range_distribution(torch_cuda, hip):
     """The generator's own ranges (uniform 0.2..300 m, 10% no-return): about
     57 of 1,536 rays per environment fall inside the window, so every
@@ -172,23 +186,29 @@ def test_huge_finite_inputs(torch_cuda, hip):
     cos(atan2(-8.5e37, -18.3)) ~ -4e-8) and the reference's Inf -> +-1 / NaN
     -> 0 mapping makes the sign depend on last-ulp libm rounding; unclamped
     tactical values reach ~1e36, where only a relative bound means anything.
-    Required: each output within 5e-5 + 1e-5*|cpu| of the oracle, or both
-    sides saturated in {-1, 0, 1}; NaN on both sides or neither; scan exact."""
+    Required: each output within 5e-5 + 1e-5*|cpu| of the oracle, NaN on both
+    sides or neither, scan exact.  A saturated mismatch (both sides in
+    {-1, 0, 1}) is allowed only in tactical values of environments that carry
+    an input of magnitude >= 1e30, and at most 24 of them (12 measured); the
+    prior allows none."""
     note("onboard huge finite inputs")
     b = synth.make_batch(512, seed=17, variant=synth.SPECIAL)
     obs = in_window(b.obs)
     (gt, gp, gd) = run_onboard(torch_cuda, hip, obs, b.mission)
     (wt, wp, wd) = oracle.onboard(obs, b.mission)
     assert np.array_equal(gd.view(np.uint32), wd.view(np.uint32))
+    huge_env = ((np.abs(obs[:, :48]) >= 1e30).any(1) | (np.abs(b.mission) >= 1e30).any(1))
     sat = np.array([-1.0, 0.0, 1.0], np.float32)
-    for g, w, name in ((gt, wt, "tactical"), (gp, wp, "prior")):
+    for g, w, name, allowed in ((gt, wt, "tactical", 24), (gp, wp, "prior", 0)):
         both_nan = np.isnan(g) & np.isnan(w)
+        assert np.array_equal(np.isnan(g), np.isnan(w)), f"{name}: NaN pattern differs"
         gg, ww = np.nan_to_num(g, nan=9.0).astype(np.float64), np.nan_to_num(w, nan=9.0)
-        close = np.abs(gg - ww) <= TOL + 1e-5 * np.abs(ww)
-        saturated = np.isin(g, sat) & np.isin(w, sat)
-        ok = both_nan | close | saturated
-        assert ok.all(), f"{name} {np.argwhere(~ok)[:3]}"
-        note(f"{name}: {int((~close & ~both_nan).sum())} saturated sign flips of {g.size}")
+        close = both_nan | (np.abs(gg - ww) <= TOL + 1e-5 * np.abs(ww))
+        flipped = ~close & np.isin(g, sat) & np.isin(w, sat) & huge_env[:, None]
+        bad = ~close & ~flipped
+        assert not bad.any(), f"{name} {np.argwhere(bad)[:3]}"
+        note(f"{name}: {int(flipped.sum())} saturated flips of {g.size} (allowed {allowed})")
+        assert flipped.sum() <= allowed, f"{name}: {int(flipped.sum())} saturated flips"
 
 
 def test_without_diag_and_sizes(torch_cuda, hip):
@@ -221,7 +241,7 @@ def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
         n = o.shape[0]
         tac = torch.full((n, 24), float("nan"), dtype=torch.float32, device="cuda")
         pri = torch.full((n, 15), float("nan"), dtype=torch.float32, device="cuda")
-        diag = torch.full((n, 4), float("nan"), dtype=torch.float32, device="cuda")
+        diag = torch.full((n, oracle.ONBOARD_DIAG), float("nan"), dtype=torch.float32, device="cuda")
         s = torch.cuda.current_stream()
         assert hip.onboard_tactical_prior_device(o, m, tac, pri, diag, n, s) == 1
         assert hip.synchronize(s) == 1

@@ -72,7 +72,7 @@ def onboard(obs: np.ndarray, mission: np.ndarray):
     b = obs.shape[0]
     tac = np.empty((b, 24), np.float32)
     pri = np.empty((b, 15), np.float32)
-    diag = np.empty((b, 4), np.float32)
+    diag = np.empty((b, oracle.ONBOARD_DIAG), np.float32)
     for e in range(b):
         lib.orc_onboard_env(np.ascontiguousarray(obs[e]).ctypes.data,
                             np.ascontiguousarray(mission[e]).ctypes.data,
@@ -141,3 +141,81 @@ def test_device_ray_table_matches_oracle_rays():
     table = np.array(vals, np.float32).reshape(1536, 3)
     want = oracle.onboard_ray_table()
     assert np.array_equal(table.view(np.uint32), want.view(np.uint32))
+
+
+# Slalom clusters whose y centres nearly cancel: (rays, ranges, py).  Each
+# case was picked (by a search over ray subsets, ranges and py) so that the
+# reference's float sum in scan order (onboard_features.cuh:231-234) and the
+# exact sum of the same y centres fall on opposite sides of the `>= 0` test
+# that picks the slalom lane (:238).  Rays are head*768 + el*128 + azi.
+NEAR_CANCEL_CLUSTERS = [
+    ([237, 873, 1000, 1144], [1.4408971071243286, 1.5016725063323975, 1.3227245807647705,
+                              0.6429145336151123], 0.3792271316051483),
+    ([246, 499, 1009], [3.342085599899292, 3.803009510040283, 3.423144578933716],
+     -0.7291140556335449),
+    ([114, 1016, 1131, 1138], [3.4220783710479736, 3.193725824356079, 3.4032883644104004,
+                               3.3478102684020996], -0.35837867856025696),
+    ([112, 235, 370, 489, 497, 498, 502, 1143],
+     [2.823929786682129, 2.807314872741699, 1.9512736797332764, 2.423358678817749,
+      2.0962674617767334, 2.8580849170684814, 3.375103235244751, 2.353227376937866],
+     -0.13887432217597961),
+    ([489, 498, 1013, 1262], [1.67618989944458, 0.6112956404685974, 1.9383928775787354,
+                              1.0888617038726807], 0.04994655027985573),
+    ([232, 488, 1133, 1144, 1262], [1.7114628553390503, 3.331336498260498, 2.220142126083374,
+                                    2.6931021213531494, 2.596982717514038], 0.41682377457618713),
+]
+
+
+def near_cancel_rows(sweep: bool = False):
+    """Level hover rows (identity attitude) on a slalom mission whose only
+    in-window rays are the case's cluster.  With `sweep`, 588 more in-window
+    rays point backwards (azimuths 24..72 of every scan row: corridor centre
+    x < -0.35, so outside the corridor), which takes the scan past its list
+    capacity."""
+    n = len(NEAR_CANCEL_CLUSTERS)
+    obs = np.zeros((n, 4148), np.float32)
+    mission = np.zeros((n, 10), np.float32)
+    obs[:, 48:4144] = -1.0
+    for e, (rays, ranges, py) in enumerate(NEAR_CANCEL_CLUSTERS):
+        o = obs[e]
+        o[1] = py; o[2] = 8.0; o[6] = 1.0; o[40] = 0.6; o[47] = 1.0
+        o[16:20] = 0.5
+        o[24:28] = 1.0
+        if sweep:
+            for h in range(2):
+                for el in range(6):
+                    o[48 + (16 * h + el) * 128 + 24:48 + (16 * h + el) * 128 + 73] = 5.0
+        for ray, r in zip(rays, ranges):
+            h, el, a = ray // 768, (ray % 768) // 128, ray % 128
+            o[48 + (16 * h + el) * 128 + a] = r
+        mission[e, 4] = 1.0  # slalom
+    return obs, mission
+
+
+def cluster_y_centres(ray_table, rays, ranges, py):
+    """y centres of the rays at identity attitude, evaluated in float32 in the
+    reference's order (onboard_features.cuh:197-203): the rotated direction is
+    the table direction itself, y_center = (py + dy*r) + dy*1.10."""
+    f32 = np.float32
+    return [f32(f32(f32(py) + ray_table[ray, 1] * f32(r)) + ray_table[ray, 1] * f32(1.1))
+            for ray, r in zip(rays, ranges)]
+
+
+@pytest.mark.parametrize("sweep", [False, True])
+def test_cluster_y_sum_is_float_in_scan_order(sweep):
+    """diag[4]: the cluster's y centres summed in float in scan order.  On
+    these clusters an exact (or double) sum of the same values has the other
+    sign, so a sum in another order or precision fails here."""
+    import math
+    obs, mission = near_cancel_rows(sweep)
+    _, _, diag = onboard(obs, mission)
+    table = oracle.onboard_ray_table()
+    for e, (rays, ranges, py) in enumerate(NEAR_CANCEL_CLUSTERS):
+        ys = cluster_y_centres(table, rays, ranges, py)
+        s = np.float32(0.0)
+        for y in ys:
+            s = np.float32(s + y)
+        exact = math.fsum(float(y) for y in ys)
+        assert (s >= 0) != (exact >= 0), (e, s, exact)
+        assert int(diag[e, 3]) == len(rays), (e, diag[e])
+        assert diag[e, 4].view(np.uint32) == s.view(np.uint32), (e, diag[e, 4], s)

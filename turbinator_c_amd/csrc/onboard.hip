@@ -8,31 +8,37 @@
 // the execution shape that suits them:
 //
 //   * the LiDAR scan (two passes over 1,536 rays: closest return, corridor
-//     minimum, cluster membership) runs one wave per environment, 24 rays
-//     per lane, so each load instruction reads 256 contiguous LiDAR bytes
-//     and no workgroup barrier is needed; the pass over the rays is
-//     branch-free, and the two heads' rays at the same azimuth and elevation
-//     share the first two products of each rotated component; the scan
-//     results are exact reductions (the closest return as the minimum
-//     (range, ray) key = first minimum in the reference scan order) done with
-//     DPP and permlane swaps, and the cluster count from lane masks;
-//   * the tactical features and the scalar controller (mission decode,
-//     targets, landing / standard / inversion / BWB laws, cannon) run in a
-//     second kernel, one lane per environment, from the scan results: the
-//     controller's long register-heavy chain is kept apart from the scan so
-//     both keep their occupancy.
+//     minimum, cluster membership and y sum) runs one wave per environment,
+//     24 rays per lane, so each load instruction reads 256 contiguous LiDAR
+//     bytes and no workgroup barrier is needed.  The wave lists its
+//     in-window rays in ray order (ballot + lane prefix) and runs both
+//     passes over the list; above kListCap in-window rays it sweeps every
+//     slot, branch-free, with the two heads' rays at the same azimuth and
+//     elevation sharing the first two products of each rotated component.
+//     The closest return is a 32-bit wave minimum of the range bits followed
+//     by a lane-mask search for its first slot and lane (the first minimum
+//     in the reference scan order); the corridor minimum is a DPP / permlane
+//     fminf reduction; the cluster count comes from lane masks, and the
+//     cluster's y centres are added in float in ray order, as the reference
+//     does, because the sign of that sum picks the slalom lane;
+//   * the tactical features and the controller (mission decode, targets,
+//     landing / standard / inversion / BWB laws, cannon) run in a second
+//     kernel from the parked scan results: one lane per environment for the
+//     tactical features, one quad of lanes per environment for the
+//     controller (lane a evaluates arm a and a quarter of the independent
+//     transcendental calls).  The controller's long register-heavy chain is
+//     kept apart from the scan so both keep their occupancy.
 //
 // Ray directions come from a table generated at build time with the host
 // libm (gen_ray_table.c), and the scan arithmetic is evaluated without FMA
 // contraction in the reference's operation order, so the per-ray world
 // vectors, and with them the closest return, its ray index, the corridor
-// minimum and the cluster count, are reproducible bit-for-bit.
+// minimum, the cluster count and the cluster y sum, are reproducible
+// bit-for-bit against the unfused C restatement.
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
-
-#include <type_traits>
 
 #include "turbinator/training/hip_features.h"
 #include "xcd_order.h"
@@ -163,31 +169,6 @@ __device__ __forceinline__ float wave_min(float v) {
     return fminf(a, __int_as_float(o));
 }
 
-__device__ __forceinline__ double wave_sum_double(double v) {
-    auto step_dpp = [](double x, auto ctrl_tag) {
-        constexpr int C = decltype(ctrl_tag)::value;
-        const long long b = __double_as_longlong(x);
-        const int lo = dpp_partner<C>((int)(b & 0xffffffffll));
-        const int hi = dpp_partner<C>((int)(b >> 32));
-        return x + __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
-    };
-    v = step_dpp(v, std::integral_constant<int, 0xB1>{});
-    v = step_dpp(v, std::integral_constant<int, 0x4E>{});
-    v = step_dpp(v, std::integral_constant<int, 0x141>{});
-    v = step_dpp(v, std::integral_constant<int, 0x140>{});
-    long long b = __double_as_longlong(v);
-    int olo, ohi;
-    int lo = swap_pair<false>((int)(b & 0xffffffffll), olo);
-    int hi = swap_pair<false>((int)(b >> 32), ohi);
-    v = __longlong_as_double(((long long)hi << 32) | (unsigned)lo) +
-        __longlong_as_double(((long long)ohi << 32) | (unsigned)olo);
-    b = __double_as_longlong(v);
-    lo = swap_pair<true>((int)(b & 0xffffffffll), olo);
-    hi = swap_pair<true>((int)(b >> 32), ohi);
-    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo) +
-           __longlong_as_double(((long long)ohi << 32) | (unsigned)olo);
-}
-
 // Ray directions as three planes (x, y, z) of 1,536 floats in LDS.
 struct RayPlanes {
     float d[3][1536];
@@ -288,6 +269,20 @@ __device__ __forceinline__ float corridor_centre(float rwx, float rwy, float rwz
     return corridor ? x_center : __builtin_huge_valf();
 }
 
+// sum + v[l0] + v[l1] + ... in float, one rounding per term, over the lanes
+// of `members` in ascending order (onboard_features.cuh:231-234 adds each
+// cluster ray's y_center in scan order; the sign of the sum decides the
+// slalom lane at :238, so the reference's rounding sequence is kept).  The
+// loop runs on the scalar unit, one v_readlane and one add per member.
+__device__ __forceinline__ float add_in_lane_order(float sum, float v, uint64_t members) {
+    while (members) {
+        const int l = (int)__builtin_ctzll(members);
+        sum += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+        members &= members - 1;
+    }
+    return sum;
+}
+
 // onboard_features.cuh:184-234 for one environment, on one wave (24 rays per
 // lane, no workgroup barrier).
 //   * The reference maps non-finite ranges to 0 / +-1000 first; both fail
@@ -344,7 +339,7 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
     int min_ray = -1;
     float min_dx_c = 30.0f;
     int count = 0;
-    double y_sum = 0.0;
+    float y_sum = 0.0f;
     if (n <= kListCap) {
         // The list is written and read by this wave only.
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -401,11 +396,9 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
 #pragma unroll
         for (int r = 0; r < kListRounds; ++r) {
             if (64 * r >= n) break;
-            const bool in = xl[r] <= limit;
-            count += __builtin_popcountll(__builtin_amdgcn_ballot_w64(in));
-            float y = in ? yl[r] : 0.0f;
-            asm("" : "+v"(y));  // select the float, then widen (one select, not two)
-            y_sum += (double)y;
+            const uint64_t members = __builtin_amdgcn_ballot_w64(xl[r] <= limit);
+            count += __builtin_popcountll(members);
+            y_sum = add_in_lane_order(y_sum, yl[r], members);
         }
     } else {
         // Every slot.  The rays of rows el and el + 6 (heads 0 and 1) at the
@@ -454,21 +447,21 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
         __builtin_amdgcn_sched_barrier(0);
         load_ranges(next, lane, rg);
         min_dx_c = wave_min(min_dx_c);
-        // Pass 2: the cluster is counted from the lane masks (scalar unit);
-        // y is summed in double.  Adding +0.0 for the rays outside the
-        // cluster leaves the sum unchanged: it starts at +0.0 and never
-        // becomes -0.0.
+        // Pass 2: the cluster is counted from the lane masks (scalar unit)
+        // and its y values summed in ray order (slot outer, lane inner).
+        // All 24 masks are formed before the first sum: interleaving the
+        // mask compares with the member loops took the kernel from 119 to
+        // 182 VGPRs (2 waves per SIMD instead of 4).
         const float limit = min_dx_c + 1.4f;
+        uint64_t members[kScanRays];
 #pragma unroll
         for (int u = 0; u < kScanRays; ++u) {
-            const bool in = xc[u] <= limit;
-            count += __builtin_popcountll(__builtin_amdgcn_ballot_w64(in));
-            float y = in ? yc[u] : 0.0f;
-            asm("" : "+v"(y));  // select the float, then widen (one select, not two)
-            y_sum += (double)y;
+            members[u] = __builtin_amdgcn_ballot_w64(xc[u] <= limit);
+            count += __builtin_popcountll(members[u]);
         }
+#pragma unroll
+        for (int u = 0; u < kScanRays; ++u) y_sum = add_in_lane_order(y_sum, yc[u], members[u]);
     }
-    y_sum = wave_sum_double(y_sum);
     if (lane == 0) {
         const int ray = min_ray;
         const float range = min_ray >= 0 ? __uint_as_float(min_bits) : 30.0f;
@@ -486,7 +479,7 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
         }
         out.min_dx_c = min_dx_c;
         out.cluster_count = count;
-        out.cluster_y_sum = (float)y_sum;
+        out.cluster_y_sum = y_sum;
     }
 }
 
@@ -1310,11 +1303,12 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
                     }
                 }
                 if (rows.diag && a == 0) {
-                    float *d = rows.diag + env * 4;
+                    float *d = rows.diag + env * 5;
                     d[0] = s.min_r;
                     d[1] = (float)s.min_ray;
                     d[2] = s.min_dx_c;
                     d[3] = (float)s.cluster_count;
+                    d[4] = s.cluster_y_sum;
                 }
             }
         }
