@@ -14,7 +14,7 @@
  *   tactical[24], prior[15]
  *   lidar[6*2048] channel c of bin (row, az): c = 0,1 inverse range of head
  *                 c%2, c = 2,3 range/30, c = 4,5 validity
- *   luma[16384]   byte / 255 - 0.5 (fused, as the reference's GPU build)
+ *   luma[16384]   byte * fl(1/255) - 0.5, two roundings (no contraction)
  */
 #include "oracle.h"
 
@@ -57,11 +57,10 @@ void orc_actor_inputs_env(const float *obs, const float *mission, const uint8_t 
                           : (c < 4 ? (valid ? clamped / 30.0f : 1.0f) : (float)valid);
             }
     }
-    /* network_gpu.cu:482 as nvcc compiles it by default (--fmad=true; the
-     * reference's CMakeLists.txt:32-36 sets no CUDA flags): the multiply and
-     * subtract contract to one fused multiply-add.  Unfused rounding differs
-     * for 158 of the 256 byte values. */
+    /* network_gpu.cu:482 as C evaluates it: the product and the difference
+     * are rounded separately (a fused multiply-add differs for 158 of the
+     * 256 byte values). */
     if (luma && cameras)
         for (int p = 0; p < 16384; ++p)
-            luma[p] = fmaf((float)cameras[p], 1.0f / 255.0f, -0.5f);
+            luma[p] = (float)cameras[p] * (1.0f / 255.0f) - 0.5f;
 }

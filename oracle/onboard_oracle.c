@@ -7,7 +7,11 @@
  * expressions and evaluation order; built without FMA contraction.  The
  * reference pins it with 40 golden values at 5e-5 and output bounds
  * (tests/test_onboard_features.cu:19-39,55-85 of the reference), which
- * tests/test_onboard_oracle.py checks, plus invariants of the controller.
+ * tests/test_onboard_oracle.py checks.  Every mission mode of the prior and
+ * all 24 tactical outputs are further pinned by closed forms at chosen
+ * states, mirror symmetry and a second formulation of the tactical features
+ * (tests/test_onboard_prior_pins.py); the cluster y sum's float scan order
+ * by near-cancelling clusters (tests/test_onboard_oracle.py).
  *
  * Optional diagnostics (no counterpart in the reference outputs):
  *   diag[0] min_r          closest in-window LiDAR return of elevations 0..3

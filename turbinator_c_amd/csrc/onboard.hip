@@ -1389,8 +1389,9 @@ extern "C" int tb_hip_onboard_tactical_prior_device(const float *obs, const floa
 // mission values after the scan, the control kernel tactical / prior and
 // their copies.  Fusing the scan into the streaming launch was measured
 // slower: next to saturated HBM traffic the scan's dependent loads stall.  Luma is
-// one fused multiply-add, which is what nvcc's default --fmad=true makes of
-// the reference's `(float)b * (1.0f / 255.0f) - 0.5f`.
+// the reference's `(float)b * (1.0f / 255.0f) - 0.5f` with two roundings, as
+// C evaluates it (this file is built without FMA contraction, like every
+// restatement of the reference's arithmetic here).
 
 namespace {
 
@@ -1467,7 +1468,7 @@ __global__ __launch_bounds__(kStreamThreads) void actor_stream_kernel(ActorRows 
                 f32x4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    o[e] = __builtin_fmaf((float)((w >> (8 * e)) & 0xffu), 1.0f / 255.0f, -0.5f);
+                    o[e] = (float)((w >> (8 * e)) & 0xffu) * (1.0f / 255.0f) - 0.5f;
                 store_sc1(dst, 16384 * 4, t + 1024 * k, o);
             }
         }
