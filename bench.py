@@ -39,12 +39,18 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def host_threads() -> int:
+CPU_THREAD_CAP = 16  # the GPU box's CPU share for one GPU
+
+
+def affinity_cores() -> int:
     try:
-        n = len(os.sched_getaffinity(0))
+        return len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        return os.cpu_count() or 1
+
+
+def host_threads() -> int:
+    return max(1, min(affinity_cores(), CPU_THREAD_CAP))
 
 
 def make_sets(torch, nsets: int, threads: int):
@@ -221,10 +227,25 @@ def _leg_depth(torch, sets, threads, steps, out):
     def depth_call(i, s):
         o, m, d, f = dsets[i % 3]
         assert features.extract_features_depth_device(o, m, d, f, BATCH, s) == 1
+    per = _events_time(torch, depth_call, steps, 5)
+    stats = _depth_sample_parity(torch, dsets[0])
     out.append(_report("config 3 with fp32 depth cameras (16,384 envs, 3 rotating sets)",
-                       _events_time(torch, depth_call, steps, 5), BATCH,
-                       OBS_B + MISSION_B + 4 * CAMERA_B + OUT_B))
+                       per, BATCH, OBS_B + MISSION_B + 4 * CAMERA_B + OUT_B,
+                       parity_sample=stats))
     del dsets
+
+
+def _depth_sample_parity(torch, dset) -> dict:
+    """256 environments of a depth set's features against the oracle of the
+    luma bytes the depth maps to."""
+    import oracle
+    from tests.conftest import assert_feature_parity
+    o, m, d, f = dset
+    idx = torch.linspace(0, BATCH - 1, 256, device="cuda").long()
+    obs, mis = o[idx].cpu().numpy(), m[idx].cpu().numpy()
+    luma = oracle.depth_to_luma(d[idx].cpu().numpy())
+    got = f[idx].cpu().numpy()
+    return assert_feature_parity(got, oracle.features(obs, mis, luma), "bench-depth")
 
 
 def _leg_diag(torch, sets, steps, out):
@@ -320,9 +341,23 @@ def _leg_c5(torch, threads, steps, out):
     def c5_call(i, s):
         assert features.extract_features_strided_device(base, rec, base + 16592, rec,
                                                         base + 16632, rec, f5, n5, s) == 1
+    per = _events_time(torch, c5_call, max(steps // 4, 10), 3)
+    stats = _c5_sample_parity(torch, dbuf, f5, rec)
     out.append(_report("config 5: 65,536 replay records x 66,672 B, in place",
-                       _events_time(torch, c5_call, max(steps // 4, 10), 3), n5, BYTES_PER_ENV))
+                       per, n5, BYTES_PER_ENV, parity_sample=stats))
     del dbuf, f5
+
+
+def _c5_sample_parity(torch, dbuf, f5, rec) -> dict:
+    """256 records' features against the oracle on the same record bytes."""
+    import oracle
+    from tests.conftest import assert_feature_parity
+    n5 = f5.shape[0]
+    idx = np.linspace(0, n5 - 1, 256).astype(np.int64)
+    rows = dbuf.view(n5, rec)[torch.from_numpy(idx).cuda()].cpu().numpy()
+    want = oracle.features_strided(rows.reshape(-1), 256, rec, 0, 16592, 16632)
+    return assert_feature_parity(f5[torch.from_numpy(idx).cuda()].cpu().numpy(), want,
+                                 "bench-config5")
 
 
 def _leg_replay(torch, threads, steps, out):
@@ -489,6 +524,18 @@ def cpu_baseline(host0, threads: int, budget_s: float) -> dict:
                       f"threads of {cpu}; {rate * BYTES_PER_ENV / 1e9:.2f} GB/s effective"}
 
 
+def cpu_baselines(host0, threads: int, budget_s: float) -> dict:
+    """All-cores figure (the host share: the affinity set, capped at
+    CPU_THREAD_CAP threads) with the single-thread figure beside it."""
+    allc = cpu_baseline(host0, threads, budget_s)
+    one = cpu_baseline(host0, 1, budget_s)
+    allc["affinity_cores"] = affinity_cores()
+    allc["cores_cap"] = CPU_THREAD_CAP
+    allc["single_thread"] = {"value": one["value"], "unit": "envs/s", "cores": 1,
+                             "sample": one["sample"]}
+    return allc
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -499,6 +546,8 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=None,
                     help="host threads of the CPU baseline (default: the host share, at most 16)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the configuration-3 fp32-depth and configuration-5 lines")
     ap.add_argument("--suite", action="store_true",
                     help="also time the secondary workloads (stderr JSON lines)")
     ap.add_argument("--host-legs", action="store_true",
@@ -545,17 +594,32 @@ def main() -> int:
         suite(torch, sets, threads, args.steps, legs)
     elif args.host_legs:
         host_legs(threads)
+    secondary = None
+    if not args.no_secondary:
+        # BASELINE.json configurations 3 (literal fp32 depth cameras) and 5
+        # (strided replay records), each with its own roofline fraction.
+        log("[bench] secondary: configuration 3 fp32 depth, configuration 5")
+        secondary = []
+        _leg_depth(torch, sets, threads, max(args.steps // 5, 20), secondary)
+        torch.cuda.empty_cache()
+        _leg_c5(torch, threads, max(args.steps // 2, 40), secondary)
+        torch.cuda.empty_cache()
     bytes_per_call = BYTES_PER_ENV * BATCH
     achieved = bytes_per_call / per_call / 1e9
-    traffic = None
+    traffic, traffic_src = None, None
     if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+        tj = json.loads(TRAFFIC_FILE.read_text())
+        traffic = tj.get("hbm_bytes_per_launch")
+        traffic_src = (f"{TRAFFIC_FILE.relative_to(ROOT)}: stored rocprofv3 --pmc FETCH_SIZE "
+                       f"and WRITE_SIZE runs of `bench.py --no-cpu --no-secondary "
+                       f"--copy-calibration`, scaled by a 1 GiB copy; not measured in this run")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "traffic_source": traffic_src}
     cpu = None
     if not args.no_cpu:
-        log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")
-        cpu = cpu_baseline(host0, args.cpu_threads or threads, args.cpu_seconds)
+        log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget, all cores then 1 thread)")
+        cpu = cpu_baselines(host0, args.cpu_threads or threads, args.cpu_seconds)
     line = {
         "metric": METRIC,
         "value": round(BATCH / per_call, 1),
@@ -576,6 +640,7 @@ def main() -> int:
                    "wall_s_timed": round(wall_s, 4)},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
     return 0
