@@ -249,9 +249,13 @@ __device__ __forceinline__ bool in_window(float range) {
 
 // in_window as one unsigned compare of the bits: 0x3eb33334 is the least
 // float above 0.35f and 0x41380000 is 11.5f; negative values, zeros, NaN
-// and infinities all fall outside [0x3eb33334, 0x41380000).
-__device__ __forceinline__ bool in_window_bits(float range) {
-    return __float_as_uint(range) - 0x3eb33334u < 0x41380000u - 0x3eb33334u;
+// and infinities all fall outside [0x3eb33334, 0x41380000).  The listed
+// pass stores the difference `bits - kWindowLo` itself: it orders in-window
+// ranges like the ranges, and kWindowSpan marks "none".
+constexpr unsigned kWindowLo = 0x3eb33334u;             // least float above 0.35f
+constexpr unsigned kWindowSpan = 0x41380000u - kWindowLo;  // 11.5f - kWindowLo
+__device__ __forceinline__ unsigned window_offset(float range) {
+    return __float_as_uint(range) - kWindowLo;
 }
 
 // onboard_features.cuh:199-207 for one ray with rotated direction rw:
@@ -309,13 +313,16 @@ __device__ __forceinline__ float add_in_lane_order(float sum, float v, uint64_t 
 __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes &rays,
                                          const ScanFrame &f, __amdgpu_buffer_rsrc_t next,
                                          int lane, u32x2 *list, ScanResult &out) {
-    // List the in-window rays in slot order while counting them.  Once a
-    // slot's rays would overflow the list, counting stops: n then exceeds
-    // kListCap and the list is not used.
+    // List the in-window rays in slot order while counting them: entry =
+    // (range bits - kWindowLo, ray).  The slot's first entry address is
+    // uniform (scalar), so each lane's address is one shift-add of its lane
+    // prefix.  Once a slot's rays would overflow the list, counting stops:
+    // n then exceeds kListCap and the list is not used.
     int n = 0;
 #pragma unroll
     for (int u = 0; u < kScanRays; ++u) {
-        const bool in = in_window_bits(rg[u]);
+        const unsigned off = window_offset(rg[u]);
+        const bool in = off < kWindowSpan;
         const uint64_t m = __builtin_amdgcn_ballot_w64(in);
         const int next_n = n + (int)__builtin_popcountll(m);
         if (next_n > kListCap) {
@@ -327,8 +334,8 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
         unsigned pos = __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
                                                  __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
         asm volatile("" : "+v"(pos));  // formed on every lane, then selected
-        list[in ? n + pos : kListCap + lane] =
-            u32x2{__float_as_uint(rg[u]), (unsigned)(64 * u + lane)};
+        u32x2 *const slot_list = list + n;
+        *(in ? slot_list + pos : list + kListCap + lane) = u32x2{off, (unsigned)(64 * u + lane)};
         n = next_n;
     }
 
@@ -346,28 +353,28 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         load_ranges(next, lane, rg);
+        // Round r's values exist only when 64 r < n, and every later loop
+        // stops at the same bound (initialising the unused rounds cost
+        // about 35 moves per environment).
         float xl[kListRounds], yl[kListRounds];
         unsigned key[kListRounds];
         int ray_of[kListRounds];
-        unsigned lane_min = kWindowTop;
+        unsigned lane_min = kWindowSpan;
 #pragma unroll
         for (int r = 0; r < kListRounds; ++r) {
-            xl[r] = __builtin_huge_valf();
-            yl[r] = 0.0f;
-            key[r] = kWindowTop;
-            ray_of[r] = 0;
             if (64 * r < n) {
                 const int e = 64 * r + lane;
                 const u32x2 entry = list[e];
                 const bool valid = e < n;
-                // Entries past n are left from earlier environments: a range
-                // of 0 fails the window.
-                const float range = valid ? __uint_as_float(entry.x) : 0.0f;
+                // Entries past n are left from earlier environments: they
+                // read as 11.5 (kWindowSpan + kWindowLo), outside the window.
+                const unsigned off = valid ? entry.x : kWindowSpan;
+                const float range = __uint_as_float(off + kWindowLo);
                 const int ray = valid ? (int)entry.y : 0;
                 // Ray 128 row + azimuth, row = 6 head + el: el < 4 on rows
                 // 0..3 and 6..9.
                 const bool low_row = ((0x3cfu >> (ray >> 7)) & 1u) != 0u;
-                key[r] = ((int)valid & (int)low_row) ? entry.x : kWindowTop;
+                key[r] = low_row ? off : kWindowSpan;
                 ray_of[r] = ray;
                 lane_min = min(lane_min, key[r]);
                 const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
@@ -378,13 +385,15 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
                 min_dx_c = fminf(min_dx_c, xl[r]);
             }
         }
-        min_bits = wave_min_u32(lane_min);
-        if (min_bits != kWindowTop) {
+        const unsigned min_off = wave_min_u32(lane_min);
+        min_bits = min_off + kWindowLo;
+        if (min_off != kWindowSpan) {
             // The list runs in ray order, so the first round and lane
             // holding the minimum is the reference's first minimum.
 #pragma unroll
             for (int r = 0; r < kListRounds; ++r) {
-                const uint64_t hit = __builtin_amdgcn_ballot_w64(key[r] == min_bits);
+                if (64 * r >= n) break;
+                const uint64_t hit = __builtin_amdgcn_ballot_w64(key[r] == min_off);
                 if (hit) {
                     min_ray = __builtin_amdgcn_readlane(ray_of[r], (int)__builtin_ctzll(hit));
                     break;
