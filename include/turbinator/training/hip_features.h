@@ -21,7 +21,7 @@ enum {
     TB_HIP_MISSION_DIM = 10,
     TB_HIP_CAMERA_BYTES = 16384,
     TB_HIP_FEATURE_DIM = 142,
-    TB_HIP_DIAG_WORDS = 224,
+    TB_HIP_DIAG_BYTES = 432,
     TB_HIP_TACTICAL_DIM = 24,
     TB_HIP_PRIOR_DIM = 15,
     TB_HIP_ONBOARD_DIAG_DIM = 5
@@ -62,14 +62,19 @@ int tb_hip_extract_features_indexed_device(const void *obs, size_t obs_stride,
 /* The 142 features of tb_cuda_extract_features_device plus, from the same
  * single pass, per-environment diagnostics that have no counterpart in the
  * reference feature vector (training.c:107-141).  `diagnostics` receives
- * [batch, 224] 32-bit words:
- *   0..63    LiDAR sector minimum range over valid bins (float bits; -1.0 if
- *            the sector has none); valid = finite and >= 0
- *   64..127  LiDAR argmin: bin index 0..4095 of the first minimum in the
- *            reference scan order (row outer, bin inner); 0xffffffff if none
- *   128..191 LiDAR valid-bin count per sector
- *   192..207 camera quadrant minimum byte (0 when cameras is NULL)
- *   208..223 camera quadrant occupancy: bytes != 0 (0 when cameras is NULL)
+ * [batch, TB_HIP_DIAG_BYTES] bytes per environment, little-endian:
+ *   bytes 0..255    float[64]: LiDAR sector minimum range over valid bins
+ *                   (-1.0 if the sector has none); valid = finite and >= 0
+ *   bytes 256..383  uint16[64]: low byte = position of the sector's first
+ *                   minimum in the reference scan order (row outer, bin
+ *                   inner) among its 64 bins, p = 16*row + bin, 0xff if
+ *                   none; high byte = valid-bin count (0..64).  The bin
+ *                   index in the 4,096-bin block is
+ *                   head*2048 + (4*el_sector + p/16)*128 + 16*az_sector + p%16
+ *   bytes 384..399  uint8[16]: camera quadrant minimum byte (0 when cameras
+ *                   is NULL)
+ *   bytes 400..431  uint16[16]: camera quadrant occupancy, bytes != 0 (0
+ *                   when cameras is NULL)
  * Sector s = head*32 + el_sector*8 + az_sector and quadrant
  * q = cam*4 + qy*2 + qx, the feature vector's orders.  Same argument rules as
  * tb_cuda_extract_features_device; diagnostics must be 4-byte aligned. */

@@ -17,7 +17,7 @@ HERE = Path(__file__).resolve().parent
 LIB_ORACLE = HERE / "liboracle.so"
 LIB_REF = HERE / "_ref" / "libref_training.so"
 
-OBS, MISSION, CAMERA, FEATURES, DIAG_WORDS = 4148, 10, 16384, 142, 224
+OBS, MISSION, CAMERA, FEATURES, DIAG_BYTES = 4148, 10, 16384, 142, 432
 # min_r, argmin ray, min_dx_c, cluster_count, cluster_y_sum
 ONBOARD_DIAG = 5
 
@@ -182,7 +182,7 @@ def depth_to_luma(depth: np.ndarray) -> np.ndarray:
 
 def diagnostics(obs: np.ndarray, cameras: np.ndarray | None) -> np.ndarray:
     b = obs.shape[0]
-    out = np.empty((b, DIAG_WORDS), np.uint32)
+    out = np.empty((b, DIAG_BYTES), np.uint8)
     for e in range(b):
         cam = None if cameras is None else np.ascontiguousarray(cameras[e]).ctypes.data
         lib().orc_diagnostics_env(np.ascontiguousarray(obs[e], np.float32).ctypes.data, cam,

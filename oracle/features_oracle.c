@@ -136,29 +136,26 @@ void orc_depth_to_luma_array(const float *depth, uint8_t *luma, size_t n) {
     for (size_t i = 0; i < n; ++i) luma[i] = orc_depth_to_luma(depth[i]);
 }
 
-void orc_diagnostics_env(const float *obs, const uint8_t *cameras, uint32_t *diag) {
-    float *fmin = (float *)(void *)diag;
-    int32_t *arg = (int32_t *)(void *)(diag + 64);
-    int32_t *cnt = (int32_t *)(void *)(diag + 128);
-    int32_t *cmin = (int32_t *)(void *)(diag + 192);
-    int32_t *occ = (int32_t *)(void *)(diag + 208);
+void orc_diagnostics_env(const float *obs, const uint8_t *cameras, uint8_t *diag) {
     for (int head = 0; head < 2; ++head)
         for (int es = 0; es < 4; ++es)
             for (int as = 0; as < 8; ++as) {
                 const int s = head * 32 + es * 8 + as;
                 float best = 0.0f;
-                int best_i = -1, n = 0;
+                int best_p = -1, n = 0;
                 for (int el = 0; el < 4; ++el)
                     for (int az = 0; az < 16; ++az) {
                         const int bin = head * 2048 + (es * 4 + el) * 128 + as * 16 + az;
                         const float r = obs[48 + bin];
                         if (!isfinite(r) || r < 0.0f) continue;
                         ++n;
-                        if (best_i < 0 || r < best) { best = r; best_i = bin; }
+                        if (best_p < 0 || r < best) { best = r; best_p = el * 16 + az; }
                     }
-                fmin[s] = best_i < 0 ? -1.0f : best;
-                arg[s] = best_i;
-                cnt[s] = n;
+                const float m = best_p < 0 ? -1.0f : best;
+                const uint16_t word = (uint16_t)((best_p < 0 ? 0xff : best_p) | (n << 8));
+                memcpy(diag + 4 * s, &m, 4);
+                diag[256 + 2 * s] = (uint8_t)(word & 0xff);
+                diag[256 + 2 * s + 1] = (uint8_t)(word >> 8);
             }
     for (int q = 0; q < 16; ++q) {
         const int cam = q / 4, qy = (q / 2) % 2, qx = q % 2;
@@ -173,8 +170,9 @@ void orc_diagnostics_env(const float *obs, const uint8_t *cameras, uint32_t *dia
                     n += v != 0;
                 }
         }
-        cmin[q] = lo;
-        occ[q] = n;
+        diag[384 + q] = (uint8_t)lo;
+        diag[400 + 2 * q] = (uint8_t)(n & 0xff);
+        diag[400 + 2 * q + 1] = (uint8_t)(n >> 8);
     }
 }
 

@@ -19,7 +19,7 @@ enum {
     ORC_MISSION = 10,
     ORC_CAMERA = 16384,
     ORC_FEATURES = 142,
-    ORC_DIAG_WORDS = 224
+    ORC_DIAG_BYTES = 432
 };
 
 /* One environment, reference src/training/training.c:102-142. */
@@ -44,13 +44,14 @@ void orc_lidar_feature_array(const float *in, float *out, size_t n, int threads)
 uint8_t orc_depth_to_luma(float depth_m);
 void orc_depth_to_luma_array(const float *depth, uint8_t *luma, size_t n);
 
-/* Per-environment diagnostics with no counterpart in the 142-vector:
- * words 0..63    LiDAR sector minimum over valid bins (float, -1 if none)
- * words 64..127  LiDAR argmin bin index 0..4095 (int32, first in scan order, -1)
- * words 128..191 LiDAR valid-bin count (int32)
- * words 192..207 camera quadrant minimum byte (int32, 0 when cameras NULL)
- * words 208..223 camera quadrant occupancy: bytes != 0 (int32)              */
-void orc_diagnostics_env(const float *obs, const uint8_t *cameras, uint32_t *diag);
+/* Per-environment diagnostics with no counterpart in the 142-vector, one
+ * 432-byte row (little-endian):
+ * bytes 0..255    float[64] LiDAR sector minimum over valid bins (-1 if none)
+ * bytes 256..383  uint16[64] first-minimum position p = 16*row + bin inside
+ *                 the sector (scan order; 0xff if none) | valid count << 8
+ * bytes 384..399  uint8[16] camera quadrant minimum byte (0 when cameras NULL)
+ * bytes 400..431  uint16[16] camera quadrant occupancy: bytes != 0          */
+void orc_diagnostics_env(const float *obs, const uint8_t *cameras, uint8_t *diag);
 
 /* Onboard tactical (24) and prior (15) features, reference
  * src/network/onboard_features.cuh:25-519.  `diag` (nullable) receives

@@ -239,12 +239,12 @@ def run_diag(torch, hip, obs, mission, cameras):
     d_mis = torch.from_numpy(np.ascontiguousarray(mission)).cuda()
     d_cam = None if cameras is None else torch.from_numpy(np.ascontiguousarray(cameras)).cuda()
     out = torch.full((b, 142), float("nan"), dtype=torch.float32, device="cuda")
-    diag = torch.full((b, 224), -7, dtype=torch.int32, device="cuda")
+    diag = torch.full((b, oracle.DIAG_BYTES), 0xa5, dtype=torch.uint8, device="cuda")
     s = torch.cuda.current_stream()
     torch.cuda.synchronize()
     assert hip.extract_features_diagnostics_device(d_obs, d_mis, d_cam, out, diag, b, s) == 1
     assert hip.synchronize(s) == 1
-    return out.cpu().numpy(), diag.cpu().numpy().view(np.uint32)
+    return out.cpu().numpy(), diag.cpu().numpy()
 
 
 @pytest.mark.parametrize("variant,batch", [(synth.EDGE_QUARTERS, 4096), (synth.SPECIAL, 512),
@@ -259,8 +259,9 @@ def test_diagnostics_bit_exact(torch_cuda, hip, variant, batch):
     assert not bad.size, f"diag word {bad[0]}: gpu {diag[tuple(bad[0])]:#x} " \
                          f"cpu {want[tuple(bad[0])]:#x} ({len(bad)} words differ)"
     if variant == synth.EDGE_QUARTERS:
-        assert np.all(diag[:1024, 64:128] == 0xffffffff)          # Q1: no valid bin
-        assert np.all(diag[1024:2048, 192:208] == 207)            # Q2: constant camera
+        assert np.all(diag[:1024, 256:384:2] == 0xff)             # Q1: no valid bin
+        assert np.all(diag[:1024, 257:384:2] == 0)                # ... and no count
+        assert np.all(diag[1024:2048, 384:400] == 207)            # Q2: constant camera
 
 
 def test_diagnostics_null_cameras(torch_cuda, hip):
@@ -268,7 +269,7 @@ def test_diagnostics_null_cameras(torch_cuda, hip):
     b = synth.make_batch(128, seed=5)
     feats, diag = run_diag(torch_cuda, hip, b.obs, b.mission, None)
     assert np.array_equal(diag, oracle.diagnostics(b.obs, None))
-    assert np.all(diag[:, 192:] == 0)
+    assert np.all(diag[:, 384:] == 0)
 
 
 def run_depth(torch, hip, obs, mission, depth):

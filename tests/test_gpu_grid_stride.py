@@ -94,7 +94,7 @@ def test_features_device_and_diagnostics(torch_cuda, hip):
     def run(o, m, c):
         n = o.shape[0]
         out, out2 = nan_rows(torch, n, 142), nan_rows(torch, n, 142)
-        diag = torch.full((n, 224), -7, dtype=torch.int32, device="cuda")
+        diag = torch.full((n, oracle.DIAG_BYTES), 0xa5, dtype=torch.uint8, device="cuda")
         assert hip.extract_features_device(o, m, c, out, n, s) == 1
         assert hip.extract_features_diagnostics_device(o, m, c, out2, diag, n, s) == 1
         assert hip.synchronize(s) == 1
@@ -104,8 +104,7 @@ def test_features_device_and_diagnostics(torch_cuda, hip):
     assert_feature_parity(small[0].cpu().numpy(), oracle.features(b.obs, b.mission, b.cameras),
                           "small")
     assert torch.equal(small[0].view(torch.int32), small[1].view(torch.int32))
-    assert np.array_equal(small[2].cpu().numpy().view(np.uint32),
-                          oracle.diagnostics(b.obs, b.cameras))
+    assert np.array_equal(small[2].cpu().numpy(), oracle.diagnostics(b.obs, b.cameras))
     big_obs, big_mis, big_cam = tile(obs, batch), tile(mis, batch), tile(cam, batch)
     big = run(big_obs, big_mis, big_cam)
     del big_obs, big_mis, big_cam

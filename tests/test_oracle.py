@@ -200,26 +200,47 @@ def test_golden_c4_covers_every_quarter():
 
 def numpy_diagnostics(obs: np.ndarray, cameras: np.ndarray | None) -> np.ndarray:
     """Independent formulation of orc_diagnostics_env with numpy reshapes:
-    np.argmin returns the first occurrence, in scan order (row, bin)."""
+    np.argmin returns the first occurrence, in scan order (row, bin); the
+    432-byte row is assembled from little-endian views."""
     b = obs.shape[0]
-    out = np.zeros((b, 224), np.uint32)
     lid = obs[:, 48:4144].reshape(b, 2, 4, 4, 8, 16)          # env,head,es,el,as,az
     sec = lid.transpose(0, 1, 2, 4, 3, 5).reshape(b, 64, 64)  # env,sector,(el,az)
-    binidx = np.arange(4096).reshape(2, 4, 4, 8, 16).transpose(0, 1, 3, 2, 4).reshape(64, 64)
     valid = np.isfinite(sec) & (sec >= 0)
     masked = np.where(valid, sec, np.inf)
     arg = np.argmin(masked, axis=2)
     anyv = valid.any(axis=2)
     mins = np.take_along_axis(sec, arg[..., None], axis=2)[..., 0]
-    out[:, 0:64] = np.where(anyv, mins, np.float32(-1.0)).astype(np.float32).view(np.uint32)
-    out[:, 64:128] = np.where(anyv, binidx[np.arange(64)[None, :], arg], -1).astype(
-        np.int32).view(np.uint32)
-    out[:, 128:192] = valid.sum(axis=2)
+    fmin = np.where(anyv, mins, np.float32(-1.0)).astype("<f4")
+    word = (np.where(anyv, arg, 0xff) | (valid.sum(axis=2) << 8)).astype("<u2")
+    cmin = np.zeros((b, 16), np.uint8)
+    occ = np.zeros((b, 16), "<u2")
     if cameras is not None:
         q = cameras.reshape(b, 4, 2, 32, 2, 32).transpose(0, 1, 2, 4, 3, 5).reshape(b, 16, 1024)
-        out[:, 192:208] = q.min(axis=2)
-        out[:, 208:224] = (q != 0).sum(axis=2)
-    return out
+        cmin = q.min(axis=2).astype(np.uint8)
+        occ = (q != 0).sum(axis=2).astype("<u2")
+    return np.concatenate([fmin.view(np.uint8), word.view(np.uint8), cmin, occ.view(np.uint8)],
+                          axis=1)
+
+
+def diag_bin_index(diag: np.ndarray) -> np.ndarray:
+    """[B, 64] bin index 0..4095 of each sector's first minimum (-1 if none),
+    decoded from the position byte as the header documents."""
+    pos = diag[:, 256:384:2].astype(np.int64)
+    s = np.arange(64)
+    head, es, az_s = s // 32, (s // 8) % 4, s % 8
+    idx = head * 2048 + (4 * es + pos // 16) * 128 + 16 * az_s + pos % 16
+    return np.where(pos == 0xff, -1, idx)
+
+
+def test_diag_bin_index_decodes_to_the_minimum():
+    b = synth.make_batch(8, seed=71, variant=synth.TIED_MINIMA)
+    d = oracle.diagnostics(b.obs, b.cameras)
+    idx = diag_bin_index(d)
+    fmin = d[:, :256].view("<f4")
+    for e in range(8):
+        for s in range(64):
+            if idx[e, s] >= 0:
+                assert b.obs[e, 48 + idx[e, s]] == fmin[e, s]
 
 
 @pytest.mark.parametrize("variant", [0, 3, 4, 5])

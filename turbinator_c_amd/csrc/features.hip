@@ -40,6 +40,12 @@ constexpr int kBlockThreads = 256;
 constexpr int kStagePitch = 68;  // 16-byte units per LDS stage chunk row
 constexpr unsigned kMaxBlocks = 1u << 20;
 constexpr size_t kMaxBatch = 0x7fffffffu;
+// Diagnostics row (bytes): sector minimum as float [0, 256), per sector a
+// 16-bit word (first-minimum position inside the sector | valid count << 8)
+// [256, 384), camera quadrant minimum byte [384, 400), camera quadrant
+// nonzero count as 16 bits [400, 432).
+constexpr int kDiagBytes = TB_HIP_DIAG_BYTES;
+constexpr int kDiagArgCount = 256, kDiagCamMin = 384, kDiagCamOcc = 400;
 
 // L = log1pf(120.0f) = 0x1.32ee3cp+2 as the reference evaluates it (glibc
 // and GCC's constant folding agree; it is the correctly rounded float of
@@ -64,7 +70,7 @@ struct Rows {
     const float *depth;  // fp32 depth cameras [batch, 16384] metres (DEPTH kernels)
     size_t depth_stride;
     float *out;
-    uint32_t *diag;  // optional [batch, 224] diagnostics words (DIAG kernels)
+    unsigned char *diag;  // optional [batch, kDiagBytes] diagnostics rows (DIAG kernels)
     const uint32_t *index;  // optional: output row e reads input row index[e]
     size_t capacity;        // input rows available when index is set
     size_t batch;
@@ -368,7 +374,8 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
             out[126 + w * 4 + lane] = 0.0f;
         }
         if constexpr (DIAG) {  // camera words are dead after this
-            uint32_t *diag = rows.diag + env * 224;
+            unsigned char *diag = rows.diag + env * kDiagBytes;
+            unsigned short *occ = reinterpret_cast<unsigned short *>(diag + kDiagCamOcc);
             if (has_cameras) {
                 const unsigned top_min = min_same_qx(bytes_min(px[1], bytes_min(px[0], 255u)));
                 const unsigned bot_min = min_same_qx(bytes_min(px[3], bytes_min(px[2], 255u)));
@@ -376,14 +383,14 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
                 const unsigned bot_occ = sum_same_qx(bytes_nonzero(px[3], bytes_nonzero(px[2], 0u)));
                 if (lane == 0 || lane == 2) {
                     const int q = w * 4 + (lane >> 1);
-                    diag[192 + q] = top_min;
-                    diag[192 + q + 2] = bot_min;
-                    diag[208 + q] = top_occ;
-                    diag[208 + q + 2] = bot_occ;
+                    diag[kDiagCamMin + q] = (unsigned char)top_min;
+                    diag[kDiagCamMin + q + 2] = (unsigned char)bot_min;
+                    occ[q] = (unsigned short)top_occ;
+                    occ[q + 2] = (unsigned short)bot_occ;
                 }
             } else if (lane < 4) {
-                diag[192 + w * 4 + lane] = 0u;
-                diag[208 + w * 4 + lane] = 0u;
+                diag[kDiagCamMin + w * 4 + lane] = 0u;
+                occ[w * 4 + lane] = 0u;
             }
         }
 
@@ -415,14 +422,15 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
                 sum += f.w;
             }
             out[62 + lane] = sum / 64.0f;
-            if constexpr (DIAG) {
+        }
+        if (DIAG && w == 1) {
+            // The diagnostics reduction runs on wave 1, beside wave 0's sums.
                 // Chunks in increasing c are in scan order (row outer, bin
-                // inner), so a strict < keeps the first minimum.
-                // Sector `lane` (head, elevation sector, azimuth sector);
-                // chunk c holds its elevation row 4 es + c / 4, bins
-                // 4 (c % 4) .. + 3 of the azimuth sector.
-                const unsigned sector_bin0 =
-                    (lane >> 5) * 2048 + ((lane >> 3) & 3) * 512 + (lane & 7) * 16;
+                // inner), so a strict < keeps the first minimum.  Chunk c of
+                // sector `lane` holds its elevation row c / 4 (within the
+                // sector), bins 4 (c % 4) .. + 3 of the azimuth sector, so
+                // the position of chunk bin pos (1-based) inside the
+                // sector's 64 bins, row-major, is 4 c + pos - 1.
                 float best = 0.0f;
                 unsigned first = 0u, count = 0u;
 #pragma unroll
@@ -433,14 +441,16 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
                     count += part.y >> 16;
                     const bool take = (int)(pos != 0u) & ((int)(first == 0u) | (int)(m < best));
                     best = take ? m : best;
-                    first = take ? sector_bin0 + (c >> 2) * 128 + 4 * (c & 3) + pos : first;
+                    first = take ? 4 * c + pos : first;
                 }
-                uint32_t *diag = rows.diag + env * 224;
-                diag[lane] = first == 0u ? __float_as_uint(-1.0f) : __float_as_uint(best);
-                diag[64 + lane] = first == 0u ? 0xffffffffu : first - 1u;
-                diag[128 + lane] = count;
+                unsigned char *diag = rows.diag + env * kDiagBytes;
+                reinterpret_cast<float *>(diag)[lane] = first == 0u ? -1.0f : best;
+                // Two sectors' 16-bit words per 32-bit store (even lanes).
+                const unsigned word = ((first - 1u) & 0xffu) | (count << 8);
+                const unsigned pair = word | (__shfl_xor(word, 1) << 16);
+                if ((lane & 1) == 0)
+                    reinterpret_cast<unsigned *>(diag + kDiagArgCount)[lane >> 1] = pair;
             }
-        }
         // The stage is reused by this block's next environment, if any.
         if (env + gridDim.x < rows.batch) __syncthreads();
     }
@@ -545,7 +555,7 @@ extern "C" int tb_hip_extract_features_diagnostics_device(const float *obs, cons
     rows.depth = nullptr;
     rows.depth_stride = 0;
     rows.out = features;
-    rows.diag = static_cast<uint32_t *>(diagnostics);
+    rows.diag = static_cast<unsigned char *>(diagnostics);
     rows.index = nullptr;
     rows.capacity = 0;
     rows.batch = batch_size;

@@ -20,7 +20,7 @@ OBS_DIM = 4148
 MISSION_DIM = 10
 CAMERA_BYTES = 16384
 FEATURE_DIM = 142
-DIAG_WORDS = 224
+DIAG_BYTES = 432
 TACTICAL_DIM = 24
 PRIOR_DIM = 15
 
