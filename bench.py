@@ -149,11 +149,18 @@ def verify_sample(torch, sets, host0) -> dict:
 
 
 def _events_time(torch, launch, steps: int, warmup: int) -> float:
-    """Seconds per call of `launch(i)` on the current stream (HIP events)."""
+    """Seconds per call of `launch(i)` on the current stream (HIP events),
+    after at least `warmup` untimed calls and at least SUITE_WARMUP_S of
+    untimed calls (the first ~30 ms of a workload that follows host-side
+    work run slower: the diagnostics kernel measured 117 -> 95 us per call
+    over its first 250 calls)."""
     stream = torch.cuda.current_stream()
-    for i in range(warmup):
-        launch(i, stream)
-    torch.cuda.synchronize()
+    i, t0 = 0, time.perf_counter()
+    while i < warmup or time.perf_counter() - t0 < SUITE_WARMUP_S:
+        for _ in range(max(warmup, 1)):
+            launch(i, stream)
+            i += 1
+        torch.cuda.synchronize()
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record(stream)
@@ -177,9 +184,9 @@ def _report(name: str, per_call: float, envs: int, bytes_per_env: int | None, **
 
 
 SUITE_LEGS = ("depth", "diag", "onboard", "actor_prep", "sac_actor", "c5", "replay", "host")
-# Untimed calls before each secondary workload: a new workload's first tens of
-# calls on a box run slower (measured up to 25% over the first 5 to 50 calls).
+# Untimed calls (and seconds of them) before each secondary workload.
 SUITE_WARMUP = 20
+SUITE_WARMUP_S = 0.1
 
 
 def suite(torch, sets, threads: int, steps: int, legs=SUITE_LEGS) -> list:
