@@ -124,13 +124,13 @@ __device__ __forceinline__ float tanh_hidden(float x) {
     return __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
 }
 
-// A workgroup's four waves share one group of 16 environments: in every
-// layer wave w computes output tiles w, w + 4, w + 8, ... (the 142 -> hidden
-// and hidden -> hidden layers) or tile w (the hidden -> 30 layer, waves 0
-// and 1), and the finished tiles go through LDS to all four waves as the next
-// layer's input fragments.  With a 16-environment group per workgroup a
-// 16,384-row batch is 1,024 workgroups, four per CU, so each SIMD holds four
-// waves whose matrix-core work, weight loads and epilogues overlap.
+// A workgroup's four waves share two groups of 16 environments: in the
+// 142 -> hidden and hidden -> hidden layers wave w computes output tiles
+// w, w + 4, w + 8, ... for both groups; in the hidden -> 30 layer (two tiles
+// per group) wave w computes tile w % 2 of group w / 2.  The finished tiles
+// go through LDS to all four waves as the next layer's input fragments.  A
+// 16,384-row batch is 512 workgroups, two per CU, so every SIMD holds two
+// waves with the same matrix-core work.
 constexpr int kWaves = 4;
 constexpr int kGroups = 2;  // groups of 16 environments per workgroup pass
 
@@ -273,6 +273,7 @@ __device__ __forceinline__ void store_tiles(f32x4 *rows, const f32x4 (&h)[TPW][G
 template <int HT, int G>
 __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
     constexpr int TPW = (HT + kWaves - 1) / kWaves;  // hidden tiles per wave
+    static_assert(kWaves == 2 * G, "the hidden -> 30 layer gives each wave one (tile, group)");
     constexpr int E = 16 * G;                        // environments per workgroup pass
     // Row stride of the workgroup's LDS rows (floats): the 144 padded
     // features or the padded hidden activations, plus 4 so rows start on
@@ -352,26 +353,27 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
             store_tiles<TPW, G, HT, S>(buf[0], h, w, lane);
         }
         __syncthreads();
+        // The hidden -> 30 layer has two output tiles per group: wave w
+        // takes tile w % 2 of group w / 2, so the four waves share it evenly.
+        const int tile2 = w & 1, group2 = w >> 1;
         LayerWeights<1> lw2;
         {
             f32x4 h[TPW][G];
             layer_tiles<HT, HT, TPW, G, true, S>(wrs, a.w_off[1], buf[0], lw1, h, w, lane);
-            if (w < 2) layer_prefetch<HT, 2, 1>(wrs, a.w_off[2], a.b_off[2], w, lane, lw2);
+            layer_prefetch<HT, 2, 1>(wrs, a.w_off[2], a.b_off[2], tile2, lane, lw2);
             store_tiles<TPW, G, HT, S>(buf[1], h, w, lane);
         }
         __syncthreads();
-        if (w < 2) {
-            f32x4 r[1][G];
-            layer_tiles<HT, 2, 1, G, false, S>(wrs, a.w_off[2], buf[1], lw2, r, w, lane);
+        {
+            f32x4 r[1][1];
+            layer_tiles<HT, 2, 1, 1, false, S>(wrs, a.w_off[2], buf[1] + group2 * 4 * S, lw2, r,
+                                               tile2, lane);
+            const size_t env = base + 16 * group2 + j;
 #pragma unroll
-            for (int q = 0; q < G; ++q) {
-                const size_t env = base + 16 * q + j;
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int n = 16 * w + 4 * g + v;
-                    raw_s[16 * q + j][n] = r[0][q][v];
-                    if (a.raw && env < a.batch && n < kRaw) a.raw[env * kRaw + n] = r[0][q][v];
-                }
+            for (int v = 0; v < 4; ++v) {
+                const int n = 16 * tile2 + 4 * g + v;
+                raw_s[16 * group2 + j][n] = r[0][0][v];
+                if (a.raw && env < a.batch && n < kRaw) a.raw[env * kRaw + n] = r[0][0][v];
             }
         }
         __syncthreads();
