@@ -611,9 +611,29 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     const float cannon_el_lim = pi / 6.0f;
     float o[48], m[10];
 #pragma unroll
-    for (int i = 0; i < 48; ++i) o[i] = ob_obs(input_obs[i]);
+    for (int i = 0; i < 48; ++i) o[i] = input_obs[i];
 #pragma unroll
-    for (int i = 0; i < 10; ++i) m[i] = ob_mission(input_mission[i]);
+    for (int i = 0; i < 10; ++i) m[i] = input_mission[i];
+    // The staged inputs the chain reads are all taken from LDS here, at
+    // once: an empty asm on each value keeps the compiler from sinking its
+    // read to the first use, where every read cost the chain its own LDS
+    // round trip (51 waits on LDS in the kernel before, 29 after).
+    float arm_in[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) arm_in[k] = input_obs[16 + 4 * k + a];
+    {
+        constexpr int kUsed[] = {0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 40, 41, 44, 45, 46, 47};
+#pragma unroll
+        for (int i : kUsed) asm volatile("" : "+v"(o[i]));
+#pragma unroll
+        for (int i = 0; i < 10; ++i) asm volatile("" : "+v"(m[i]));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) asm volatile("" : "+v"(arm_in[k]));
+    }
+#pragma unroll
+    for (int i = 0; i < 48; ++i) o[i] = ob_obs(o[i]);
+#pragma unroll
+    for (int i = 0; i < 10; ++i) m[i] = ob_mission(m[i]);
     const float px = o[0], py = o[1], pz = o[2], vx = o[3], vy = o[4], vz = o[5];
     const Attitude att = attitude_of(o[6], o[7], o[8], o[9]);
     const float qw = att.qw, qx = att.qx, qy = att.qy, qz = att.qz;
@@ -625,11 +645,11 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     const float omega_norm = ob_norm3(ox, oy, oz);
 
     // Arm a of the four (this lane's); the quad exchanges the arm forces.
-    const float spool = ob_clamp(ob_obs(input_obs[16 + a]), 0.0f, 1.0f);
+    const float spool = ob_clamp(ob_obs(arm_in[0]), 0.0f, 1.0f);
     const float thrust = max_installed * (idle_frac + (1.0f - idle_frac) * spool);
-    const float outer = atan2f(ob_obs(input_obs[20 + a]), ob_obs(input_obs[24 + a]));
+    const float outer = atan2f(ob_obs(arm_in[1]), ob_obs(arm_in[2]));
     const SinCos o_sc = sin_cos(outer);
-    const float c_inner = cosf(ob_obs(input_obs[28 + a]));
+    const float c_inner = cosf(ob_obs(arm_in[3]));
     const float fz_a = thrust * o_sc.c * c_inner;
     const float ft_a = thrust * o_sc.s * c_inner;
     const Quad4 fz = quad_all(fz_a), ft = quad_all(ft_a);
@@ -1282,6 +1302,9 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
                 s.cluster_y_sum = sc[4];
                 s.min_ray = __float_as_int(sc[5]);
                 s.cluster_count = __float_as_int(sc[6]);
+                // Read from LDS before the chain, like the other inputs.
+                asm volatile("" : "+v"(s.min_r), "+v"(s.min_r_dx), "+v"(s.min_r_dy), "+v"(s.min_dx_c),
+                             "+v"(s.cluster_y_sum), "+v"(s.min_ray), "+v"(s.cluster_count));
                 const ArmOutputs n = prior_features(obs, mission, s, a);
                 // The parked result was staged before the chain; each lane
                 // now writes its arm's three values, lane 0 the cannon's.
