@@ -106,12 +106,15 @@ def scan_ray_columns():
 
 
 @pytest.mark.parametrize("counts", [(0, 1, 2, 63, 64, 65, 127, 128, 129, 200),
-                                    (255, 256, 257, 300, 640, 1000, 1535, 1536)])
+                                    (255, 256, 257, 300, 640, 1000, 1535, 1536),
+                                    (448, 500, 511, 512, 513, 520, 575, 576, 577)])
 def test_listed_and_swept_scans(torch_cuda, hip, counts):
     """Exactly k of an environment's 1,536 scan rays inside the 0.35..11.5 m
     window, at random positions: up to 512 the wave lists the in-window rays
-    and runs the passes over the list, above that it sweeps every slot.  The
-    other rays take values just outside the window or non-finite ones."""
+    and runs the passes over the list, above that it sweeps every slot (the
+    third set sits on that boundary, where the last listed slot may write
+    into the list's spare entries).  The other rays take values just outside
+    the window or non-finite ones."""
     note(f"onboard scans with k in-window rays, k in {counts}")
     per_k = 64
     batch = per_k * len(counts)

@@ -321,22 +321,24 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
     int n = 0;
 #pragma unroll
     for (int u = 0; u < kScanRays; ++u) {
+        // A slot adds at most 64 entries, so the list can be full only from
+        // slot kListCap / 64 + 1 on.
+        if (64 * u > kListCap && n > kListCap) break;
         const unsigned off = window_offset(rg[u]);
         const bool in = off < kWindowSpan;
         const uint64_t m = __builtin_amdgcn_ballot_w64(in);
-        const int next_n = n + (int)__builtin_popcountll(m);
-        if (next_n > kListCap) {
-            n = next_n;
-            break;
-        }
-        // Lanes outside the window write to their own spare entry, so the
-        // store needs no branch.
+        // The lane's list position: the running count plus the in-window
+        // lanes below it (mbcnt adds its second operand).  With n <= kListCap
+        // every position is below kListCap + 64, inside the list and its
+        // spare entries; a slot that takes the count past kListCap abandons
+        // the list, so what it wrote there is never read.  Lanes outside the
+        // window write to their own spare entry, so the store needs no
+        // branch.
         unsigned pos = __builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+                                                 __builtin_amdgcn_mbcnt_lo((unsigned)m, (unsigned)n));
         asm volatile("" : "+v"(pos));  // formed on every lane, then selected
-        u32x2 *const slot_list = list + n;
-        *(in ? slot_list + pos : list + kListCap + lane) = u32x2{off, (unsigned)(64 * u + lane)};
-        n = next_n;
+        *(list + (in ? pos : (unsigned)(kListCap + lane))) = u32x2{off, (unsigned)(64 * u + lane)};
+        n += (int)__builtin_popcountll(m);
     }
 
     // Closest return: a ray outside the window or on elevation rows 4..5
