@@ -577,9 +577,9 @@ def main() -> int:
         print(json.dumps(summary, indent=1))
         return 0
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU only (the feature path needs no "
-              "inter-GPU exchange; see DESIGN.md for how it shards). Use --gpus 1.",
-              file=sys.stderr)
+        print("bench.py: this build measures one GPU only. The feature path needs no "
+              "inter-GPU exchange: a batch shards by contiguous environment ranges, one per "
+              "GPU, each running the same kernel. Use --gpus 1.", file=sys.stderr)
         return 2
     import torch
     if not torch.cuda.is_available():

@@ -1,7 +1,7 @@
 """The CMake integration a maintainer adds to the reference tree builds.
 
 A throwaway CMake project (written to a temp dir) adds turbinator_c_amd/ with
-add_subdirectory, exactly as INTEGRATION.md shows for the reference's
+add_subdirectory, as a maintainer would add it to the reference's
 CMakeLists.txt, and links the reference's own tests/test_cuda_features.c and
 src/training/training.c (compiled from /root/reference, which exists only in
 the build container) against the turbinator_hip target.  Nothing is run: the
