@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.test_onboard_oracle import GOLDEN, near_cancel_rows, reference_rows
+from tests.test_onboard_oracle import GOLDEN, near_cancel_rows, reference_rows, signed_zero_rows
 from turbinator_c_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -143,6 +143,52 @@ def test_listed_and_swept_scans(torch_cuda, hip, counts):
     got = run_onboard(torch_cuda, hip, obs, b.mission)
     stats = compare(got, oracle.onboard(obs, b.mission), f"counts{counts}")
     note(f"counts {counts}: {stats}")
+
+
+@pytest.mark.parametrize("sweep", [False, True])
+def test_corridor_minimum_signed_zero_ties(torch_cuda, hip, sweep):
+    """Corridor centres that tie at +0 and -0 in either order: the scan
+    diagnostics (the corridor minimum's sign included) must be bit-exact on
+    the listed and the swept pass."""
+    note(f"onboard signed-zero corridor ties, sweep={sweep}")
+    obs, mission, _ = signed_zero_rows(sweep)
+    got = run_onboard(torch_cuda, hip, obs, mission)
+    stats = compare(got, oracle.onboard(obs, mission), f"signed zero sweep={sweep}")
+    note(f"signed zero sweep={sweep}: {stats}")
+
+
+def test_signed_zero_tie_in_edge_batch(torch_cuda, hip):
+    """The configuration-4 edge batch (seed 90193) whose environment 770
+    has corridor centres +0 (first in ray order) and -0: it exposed a plain
+    wave minimum, which returned -0."""
+    note("onboard edge batch with a signed-zero corridor tie")
+    b = synth.make_batch(1024, seed=90193, variant=synth.EDGE_QUARTERS, threads=16)
+    obs = b.obs.copy()
+    obs[np.abs(obs) == np.float32(3e38)] = np.float32(7.5)
+    mission = b.mission.copy()
+    mission[np.abs(mission) == np.float32(3e38)] = np.float32(0.25)
+    want = oracle.onboard(obs, mission)
+    assert want[2][770, 2] == 0.0 and not np.signbit(want[2][770, 2])
+    compare(run_onboard(torch_cuda, hip, obs, mission), want, "edge seed 90193")
+
+
+@pytest.mark.parametrize("seed", [90393, 91266, 91848, 92818])
+def test_angle_wraps_near_pi(torch_cuda, hip, seed):
+    """Non-finite and zero attitude inputs give yaws within an ulp of +-pi
+    (e.g. quaternion (0, ., ., -inf)); which side of pi atan2 rounds to
+    decides the wrapped yaw error (about -pi or +pi) and with it the torques,
+    so an atan2 one ulp off flips whole prior rows.  Each of these batches
+    held such an environment when the kernels used the single-precision
+    atan2 there; near pi they now round correctly, as the host atan2f does."""
+    note(f"onboard special batch seed {seed}: angle wraps near pi")
+    b = synth.make_batch(1024, seed=seed, variant=synth.SPECIAL, threads=16)
+    obs = in_window(b.obs)
+    obs[np.abs(obs) == np.float32(3e38)] = np.float32(7.5)
+    mission = b.mission.copy()
+    mission[np.abs(mission) == np.float32(3e38)] = np.float32(0.25)
+    stats = compare(run_onboard(torch_cuda, hip, obs, mission), oracle.onboard(obs, mission),
+                    f"special seed {seed}")
+    note(f"special seed {seed}: {stats}")
 
 
 @pytest.mark.parametrize("sweep", [False, True])

@@ -219,3 +219,46 @@ def test_cluster_y_sum_is_float_in_scan_order(sweep):
         assert (s >= 0) != (exact >= 0), (e, s, exact)
         assert int(diag[e, 3]) == len(rays), (e, diag[e])
         assert diag[e, 4].view(np.uint32) == s.view(np.uint32), (e, diag[e, 4], s)
+
+
+def signed_zero_rows(sweep: bool = False):
+    """Rows whose corridor centres tie at +0 and -0.  The attitude
+    quaternion (1, -1, -1, 1) normalises to exactly +-0.5, so the first
+    rotation row is exactly (0, 0, -1) and a ray of zero elevation (rows 0 of
+    head 0, dz = +0, and of head 1, dz = -0) has rotated x +0 or -0 by the
+    signs of its direction terms: ray 0 (dx, dy > 0) gives +0, ray 70
+    (dx, dy < 0) -0 and ray 768 (head 1) +0.  Row 0 lists rays 0 then 70 (the
+    reference keeps +0), row 1 rays 70 then 768 (it keeps -0), row 2 only
+    ray 70.  With `sweep` every other scan ray is in the window at 11 m
+    (outside the corridor), which takes the scan past its list capacity."""
+    cases = [(0, 70), (70, 768), (70,)]
+    obs = np.zeros((len(cases), 4148), np.float32)
+    mission = np.zeros((len(cases), 10), np.float32)
+    obs[:, 48:4144] = -1.0
+    for e, rays in enumerate(cases):
+        o = obs[e]
+        o[2] = 8.0; o[6:10] = (1.0, -1.0, -1.0, 1.0); o[40] = 0.6; o[47] = 1.0
+        o[16:20] = 0.5
+        o[24:28] = 1.0
+        if sweep:
+            for h in range(2):
+                for el in range(6):
+                    o[48 + (16 * h + el) * 128:48 + (16 * h + el) * 128 + 128] = 11.0
+        for ray in rays:
+            h, el, a = ray // 768, (ray % 768) // 128, ray % 128
+            o[48 + (16 * h + el) * 128 + a] = 0.5
+        mission[e, 4] = 1.0  # slalom
+    return obs, mission, cases
+
+
+@pytest.mark.parametrize("sweep", [False, True])
+def test_corridor_minimum_keeps_the_first_signed_zero(sweep):
+    """diag[2]: the reference's strict < over corridor centres in ray order
+    (onboard_features.cuh:206) keeps the first of a +0 / -0 tie, which a
+    plain minimum (that may prefer -0) does not."""
+    obs, mission, cases = signed_zero_rows(sweep)
+    _, _, diag = onboard(obs, mission)
+    assert diag[:, 2].tolist() == [0.0, 0.0, 0.0]
+    assert np.signbit(diag[:, 2]).tolist() == [False, True, True]
+    assert diag[:, 3].tolist() == [float(len(c)) for c in cases]
+    assert diag[:, 0].tolist() == [0.5, 0.5, 0.5] and diag[:, 1].tolist() == [0.0, 70.0, 70.0]

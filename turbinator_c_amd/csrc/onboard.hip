@@ -101,9 +101,26 @@ __device__ __forceinline__ SinCos sin_cos(float x) {
     sincosf(x, &r.s, &r.c);
     return r;
 }
+// atan2f, except that a result within a few ulps of +-pi is rounded
+// correctly.  Near +-pi the float result's side of pi decides the angle
+// wraps below (a yaw of 3.1415925 and one of 3.1415927 give wrapped errors of
+// about -pi and +pi, and the controller's torques flip with them), and there
+// the single-precision routine can be one ulp from the correctly rounded
+// value, which the host libm's atan2f returns.  In that range x < 0 and
+// |y| <= 7e-7 |x|, so atan2(y, x) = sign(y) (pi - t) with t = |y / x| and
+// atan(t) = t to 1e-19: pi - t in double, rounded once, is the correctly
+// rounded result (tests/csrc/check_atan2_near_pi.c compares it with the
+// double-precision atan2 and the host atan2f on 1.8e8 such arguments).
+// y = +-0 keeps atan2f's exact +-pi.
+__device__ __forceinline__ float ob_atan2(float y, float x) {
+    const float r = atan2f(y, x);
+    if (__builtin_expect(!(fabsf(r) >= 3.1415920f) || y == 0.0f, 1)) return r;
+    const double t = fabs((double)y / (double)x);
+    return copysignf((float)(3.14159265358979323846 - t), y);
+}
 __device__ __forceinline__ float ob_wrap(float target, float current) {
     const SinCos d = sin_cos(target - current);
-    return atan2f(d.s, d.c);
+    return ob_atan2(d.s, d.c);
 }
 __device__ __forceinline__ float ob_norm3(float x, float y, float z) {
     return sqrtf(x * x + y * y + z * z);
@@ -305,7 +322,9 @@ __device__ __forceinline__ float add_in_lane_order(float sum, float v, uint64_t 
 //     which gives the value pass 1 formed (see the pair identity below).
 //   * Pass 1 keeps each ray's corridor centre (x = +inf outside the window or
 //     the corridor), so pass 2 is a compare-and-add.  The reference's
-//     strict-< update over corridor rays is the minimum of their centres.
+//     strict-< update over corridor rays is the minimum of their centres,
+//     except that of a +0 and a -0 it keeps the first in ray order, which a
+//     search over the zero centres restores when the minimum is zero.
 //   * Once the ranges are consumed (listed, or swept by pass 1), the
 //     registers take the next environment's (`next`, a 0-byte resource when
 //     there is none): they have the rest of this environment to arrive.
@@ -403,6 +422,19 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
             }
         }
         min_dx_c = wave_min(min_dx_c);
+        if (min_dx_c == 0.0f) {
+            // +0 and -0 tie; the reference keeps the first in ray order.
+#pragma unroll
+            for (int r = 0; r < kListRounds; ++r) {
+                if (64 * r >= n) break;
+                const uint64_t zero = __builtin_amdgcn_ballot_w64(xl[r] == 0.0f);
+                if (zero) {
+                    min_dx_c = __int_as_float(__builtin_amdgcn_readlane(
+                        __float_as_int(xl[r]), (int)__builtin_ctzll(zero)));
+                    break;
+                }
+            }
+        }
         const float limit = min_dx_c + 1.4f;
 #pragma unroll
         for (int r = 0; r < kListRounds; ++r) {
@@ -437,6 +469,7 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
             }
         }
         float xc[kScanRays], yc[kScanRays];
+        int min_slot = kScanRays;
 #pragma unroll
         for (int el = 0; el < 6; ++el) {
 #pragma unroll
@@ -451,13 +484,32 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
                     const int u = 2 * (6 * head + el) + half;
                     xc[u] = corridor_centre(head ? p0 - q0 : p0 + q0, head ? p1 - q1 : p1 + q1,
                                             head ? p2 - q2 : p2 + q2, rg[u], f.py, yc[u]);
-                    min_dx_c = fminf(min_dx_c, xc[u]);
+                    // The reference's strict < in ray order: the lane keeps
+                    // its minimum at the lowest slot (slots are visited head
+                    // innermost, not in ray order; equal values differ only
+                    // as +0 / -0, which is settled across lanes below).
+                    const bool lower = (int)(xc[u] < min_dx_c) |
+                                       ((int)(xc[u] == min_dx_c) & (int)(u < min_slot));
+                    min_dx_c = lower ? xc[u] : min_dx_c;
+                    min_slot = lower ? u : min_slot;
                 }
             }
         }
         __builtin_amdgcn_sched_barrier(0);
         load_ranges(next, lane, rg);
-        min_dx_c = wave_min(min_dx_c);
+        {
+            // +0 and -0 tie; the reference keeps the first in ray order
+            // (slot u holds rays 64 u .. 64 u + 63): the lowest ray among the
+            // lanes' first zeros.  Formed on every environment and selected:
+            // a branch here cost the kernel 50 VGPRs.
+            const float lane_min = min_dx_c;
+            min_dx_c = wave_min(lane_min);
+            const unsigned key =
+                lane_min == 0.0f ? 64u * (unsigned)min_slot + (unsigned)lane : ~0u;
+            const float first_zero = __int_as_float(__builtin_amdgcn_readlane(
+                __float_as_int(lane_min), (int)(wave_min_u32(key) & 63u)));
+            min_dx_c = min_dx_c == 0.0f ? first_zero : min_dx_c;
+        }
         // Pass 2: the cluster is counted from the lane masks (scalar unit)
         // and its y values summed in ray order (slot outer, lane inner).
         // All 24 masks are formed before the first sum: interleaving the
@@ -521,7 +573,7 @@ __device__ void tactical_features(const float *o, const float *m, float *t) {
     const float ct = ob_clamp(1.0f - 2.0f * (qx * qx + qy * qy), -1.0f, 1.0f);
     const float bx_x = 1.0f - 2.0f * (qy * qy + qz * qz);
     const float bx_y = 2.0f * (qx * qy + qw * qz);
-    const float yaw = atan2f(bx_y, bx_x);
+    const float yaw = ob_atan2(bx_y, bx_x);
     const SinCos yaw_sc = sin_cos(yaw);
     const float cy = yaw_sc.c, sy = yaw_sc.s;
     v[8] = cy * bz_y - sy * bz_x;
@@ -550,14 +602,14 @@ __device__ void tactical_features(const float *o, const float *m, float *t) {
     const float bx = wx + 2.0f * (uy * cz - uz * cyq);
     const float by = wy + 2.0f * (uz * cx - ux * cz);
     const float bz = wz + 2.0f * (ux * cyq - uy * cx);
-    const float az = ob_clamp(atan2f(by, bx), pi / 12.0f, pi * 5.0f / 12.0f);
-    const float el = ob_clamp(atan2f(bz, fmaxf(hypotf(bx, by), 0.2f)), -pi / 6.0f, pi / 6.0f);
+    const float az = ob_clamp(ob_atan2(by, bx), pi / 12.0f, pi * 5.0f / 12.0f);
+    const float el = ob_clamp(ob_atan2(bz, fmaxf(hypotf(bx, by), 0.2f)), -pi / 6.0f, pi / 6.0f);
     const float err = hypotf(az - o[44], el - o[45]);
     v[19] = div_const(az - pi * 0.25f, pi / 6.0f);
     v[20] = div_const(el, pi / 6.0f);
     v[21] = tanhf(err * 2.0f);
     v[22] = (o[46] <= 0.02f && o[47] > 0.01f && err < 0.26f && dist < 34.0f) ? 1.0f : -1.0f;
-    v[23] = sinf(atan2f(ry, rx) - pi * 0.25f - yaw);
+    v[23] = sinf(ob_atan2(ry, rx) - pi * 0.25f - yaw);
 #pragma unroll
     for (int i = 0; i < 24; ++i)
         t[i] = __builtin_isnan(v[i]) ? 0.0f
@@ -649,7 +701,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     // Arm a of the four (this lane's); the quad exchanges the arm forces.
     const float spool = ob_clamp(ob_obs(arm_in[0]), 0.0f, 1.0f);
     const float thrust = max_installed * (idle_frac + (1.0f - idle_frac) * spool);
-    const float outer = atan2f(ob_obs(arm_in[1]), ob_obs(arm_in[2]));
+    const float outer = ob_atan2(ob_obs(arm_in[1]), ob_obs(arm_in[2]));
     const SinCos o_sc = sin_cos(outer);
     const float c_inner = cosf(ob_obs(arm_in[3]));
     const float fz_a = thrust * o_sc.c * c_inner;
@@ -691,7 +743,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     // Independent calls of one function, one per lane of the quad: yaw, the
     // opponent bearing, the BWB roll and ground-track angles; the mission
     // offsets (atanh at the standard clamp, and the first at the BWB clamp).
-    const Quad4 angles = quad_all(atan2f(quad_pick(a, r10, m[1], r21, vy),
+    const Quad4 angles = quad_all(ob_atan2(quad_pick(a, r10, m[1], r21, vy),
                                          quad_pick(a, r00, m[2], r22, vx)));
     const float yaw = angles.v[0], opp_bearing = angles.v[1];
     const float roll_right = angles.v[2], track_yaw = angles.v[3];
@@ -744,7 +796,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
     const float aim_bx = aim_x + 2.0f * (uy * cz - uz * cyq);
     const float aim_by = aim_y + 2.0f * (uz * cx - ux * cz);
     const float aim_bz = aim_z + 2.0f * (ux * cyq - uy * cx);
-    const Quad4 bearings = quad_all(atan2f(
+    const Quad4 bearings = quad_all(ob_atan2(
         quad_pick(a, ty - py, scan.min_r_dy, aim_by, aim_bz),
         quad_pick(a, tx - px, scan.min_r_dx, aim_bx, fmaxf(hypotf(aim_bx, aim_by), 0.2f))));
     const float raw_bearing = bearings.v[0], min_az = bearings.v[1];
@@ -920,7 +972,7 @@ __device__ ArmOutputs prior_features(const float *input_obs, const float *input_
         bbx = r00 * bax + r10 * bay + r20 * baz;
         const float bby = r01 * bax + r11 * bay + r21 * baz;
         const float bbz = r02 * bax + r12 * bay + r22 * baz;
-        const Quad4 b_angles = quad_all(atan2f(
+        const Quad4 b_angles = quad_all(ob_atan2(
             quad_pick(a, gy, climb_des, bby, bbz),
             quad_pick(a, gx, fmaxf(gs, 14.0f), fmaxf(bbx, 0.2f), fmaxf(hypotf(bbx, bby), 0.2f))));
         desired_yaw_b = b_angles.v[0];
