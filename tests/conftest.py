@@ -22,6 +22,23 @@ EXACT = np.r_[0:62, 126:142]
 LIDAR = np.arange(62, 126)
 LIDAR_REL_TOL = 1e-5
 LIDAR_ABS_TOL = 1e-6
+# H2 tactical / prior: the reference test's 5e-5 (tests/test_onboard_features.cu:
+# 55-85, whose fixture values are unit-scale), plus 2e-6 relative (about 16
+# float ulps) for tactical values that unnormalised attitude inputs take far
+# past unit scale: the reference's tactical terms use the raw quaternion, so
+# feature 9 reaches about 50 for a quaternion of norm 5, where one ulp of the
+# yaw moves it by 2.4e-5.  Prior values lie in [-1, 1], where the relative
+# term adds at most 2e-6.
+H2_ABS_TOL = 5e-5
+H2_REL_TOL = 2e-6
+
+
+def h2_over(got: np.ndarray, want: np.ndarray) -> np.ndarray:
+    """Indices where H2 values miss the bar (NaN compared as 0; the callers
+    check the NaN pattern first)."""
+    g = np.nan_to_num(got).astype(np.float64)
+    w = np.nan_to_num(want).astype(np.float64)
+    return np.argwhere(np.abs(g - w) > H2_ABS_TOL + H2_REL_TOL * np.abs(w))
 
 
 def pytest_configure(config):
