@@ -5,6 +5,11 @@
   evaluates each sine/cosine pair of one angle through sincosf, so its
   results equal those of the separate calls the reference makes
   (onboard_features.cuh:18,49,119-120,210-211,325,469).
+* (float)atan2((double)y, (double)x), the controller's atan2 for the angles
+  that reach its angle wraps, is correctly rounded on 8.4e6 arguments, and
+  equals the host libm's atan2f (the oracle's) on the arguments that reach
+  the wraps' discontinuity exactly: equal, opposite and zero components and
+  results near +-pi (tests/csrc/check_atan2.hip).
 """
 from __future__ import annotations
 
@@ -24,3 +29,17 @@ def test_sincos_matches_separate_calls_for_every_float():
     proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert proc.returncode == 0, proc.stdout + proc.stderr
     assert proc.stdout.startswith("0 mismatches"), proc.stdout
+
+
+@pytest.mark.gpu
+def test_wrap_angles_match_the_host_atan2f():
+    exe = BIN / "check_atan2"
+    if not exe.exists():
+        pytest.fail(f"{exe} is not built (run __graft_entry__.build())")
+    proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    # "<n> checked, <a> differ from double atan2, <m> exact-angle arguments,
+    #  <b> differ from atan2f, <c> other arguments differ from atan2f"
+    words = proc.stdout.split("\n")[-2].split()
+    assert int(words[0]) > 8_000_000 and words[2] == "0", proc.stdout
+    assert int(words[7]) > 2_000_000 and words[10] == "0", proc.stdout

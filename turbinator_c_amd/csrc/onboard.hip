@@ -101,26 +101,25 @@ __device__ __forceinline__ SinCos sin_cos(float x) {
     sincosf(x, &r.s, &r.c);
     return r;
 }
-// atan2f, except that a result within a few ulps of +-pi is rounded
-// correctly.  Near +-pi the float result's side of pi decides the angle
-// wraps below (a yaw of 3.1415925 and one of 3.1415927 give wrapped errors of
-// about -pi and +pi, and the controller's torques flip with them), and there
-// the single-precision routine can be one ulp from the correctly rounded
-// value, which the host libm's atan2f returns.  In that range x < 0 and
-// |y| <= 7e-7 |x|, so atan2(y, x) = sign(y) (pi - t) with t = |y / x| and
-// atan(t) = t to 1e-19: pi - t in double, rounded once, is the correctly
-// rounded result (tests/csrc/check_atan2_near_pi.c compares it with the
-// double-precision atan2 and the host atan2f on 1.8e8 such arguments).
-// y = +-0 keeps atan2f's exact +-pi.
+// atan2 rounded correctly, for the angles that reach an angle wrap (yaw,
+// the goal and course bearings, the cannon azimuths, the outer gimbals).
+// ob_wrap is discontinuous where its two angles differ by pi, and that is
+// reached exactly by angles such as -3pi/4 and pi/4 (from equal or zero
+// components), or pi and a yaw of +-0: there one ulp of either angle flips
+// the wrapped error between about -pi and +pi and the controller's torques
+// with it.  The single-precision atan2f can be an ulp from the correctly
+// rounded value on such arguments; the host libm's atan2f, which the oracle
+// calls, is correctly rounded on them (equal, opposite and zero components,
+// results near +-pi: tests/csrc/check_atan2.hip), and so is the double
+// evaluation rounded once.  Elsewhere either libm may be an ulp off, which
+// moves the angles continuously.  The tactical terms and the wrap's own
+// atan2 depend on their angles continuously and keep atan2f.
 __device__ __forceinline__ float ob_atan2(float y, float x) {
-    const float r = atan2f(y, x);
-    if (__builtin_expect(!(fabsf(r) >= 3.1415920f) || y == 0.0f, 1)) return r;
-    const double t = fabs((double)y / (double)x);
-    return copysignf((float)(3.14159265358979323846 - t), y);
+    return (float)atan2((double)y, (double)x);
 }
 __device__ __forceinline__ float ob_wrap(float target, float current) {
     const SinCos d = sin_cos(target - current);
-    return ob_atan2(d.s, d.c);
+    return atan2f(d.s, d.c);
 }
 __device__ __forceinline__ float ob_norm3(float x, float y, float z) {
     return sqrtf(x * x + y * y + z * z);
@@ -573,7 +572,7 @@ __device__ void tactical_features(const float *o, const float *m, float *t) {
     const float ct = ob_clamp(1.0f - 2.0f * (qx * qx + qy * qy), -1.0f, 1.0f);
     const float bx_x = 1.0f - 2.0f * (qy * qy + qz * qz);
     const float bx_y = 2.0f * (qx * qy + qw * qz);
-    const float yaw = ob_atan2(bx_y, bx_x);
+    const float yaw = atan2f(bx_y, bx_x);
     const SinCos yaw_sc = sin_cos(yaw);
     const float cy = yaw_sc.c, sy = yaw_sc.s;
     v[8] = cy * bz_y - sy * bz_x;
@@ -602,14 +601,14 @@ __device__ void tactical_features(const float *o, const float *m, float *t) {
     const float bx = wx + 2.0f * (uy * cz - uz * cyq);
     const float by = wy + 2.0f * (uz * cx - ux * cz);
     const float bz = wz + 2.0f * (ux * cyq - uy * cx);
-    const float az = ob_clamp(ob_atan2(by, bx), pi / 12.0f, pi * 5.0f / 12.0f);
-    const float el = ob_clamp(ob_atan2(bz, fmaxf(hypotf(bx, by), 0.2f)), -pi / 6.0f, pi / 6.0f);
+    const float az = ob_clamp(atan2f(by, bx), pi / 12.0f, pi * 5.0f / 12.0f);
+    const float el = ob_clamp(atan2f(bz, fmaxf(hypotf(bx, by), 0.2f)), -pi / 6.0f, pi / 6.0f);
     const float err = hypotf(az - o[44], el - o[45]);
     v[19] = div_const(az - pi * 0.25f, pi / 6.0f);
     v[20] = div_const(el, pi / 6.0f);
     v[21] = tanhf(err * 2.0f);
     v[22] = (o[46] <= 0.02f && o[47] > 0.01f && err < 0.26f && dist < 34.0f) ? 1.0f : -1.0f;
-    v[23] = sinf(ob_atan2(ry, rx) - pi * 0.25f - yaw);
+    v[23] = sinf(atan2f(ry, rx) - pi * 0.25f - yaw);
 #pragma unroll
     for (int i = 0; i < 24; ++i)
         t[i] = __builtin_isnan(v[i]) ? 0.0f
