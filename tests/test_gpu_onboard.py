@@ -194,6 +194,27 @@ def test_angle_wraps_near_pi(torch_cuda, hip, seed):
     note(f"special seed {seed}: {stats}")
 
 
+@pytest.mark.parametrize("variant", [synth.SPECIAL, synth.CLAMP_LIMITS, synth.TIED_MINIMA,
+                                     synth.EDGE_QUARTERS])
+def test_fresh_seeds_in_window_and_raw(torch_cuda, hip, variant):
+    """Six fresh seeds of 4,096 environments per variant, with ranges scaled
+    into the scan window and as generated: the boundaries of the angle wraps
+    and the corridor minimum are reached by chance here (about one
+    environment in 10^4-10^5 of the SPECIAL variant), so these batches guard
+    them beyond the constructed cases."""
+    for k in range(6):
+        seed = 81000 + 37 * k + variant
+        b = synth.make_batch(4096, seed=seed, variant=variant, threads=16)
+        mission = b.mission.copy()
+        mission[np.abs(mission) == np.float32(3e38)] = np.float32(0.25)
+        for scaled in (True, False):
+            obs = in_window(b.obs) if scaled else b.obs.copy()
+            obs[np.abs(obs) == np.float32(3e38)] = np.float32(7.5)
+            label = f"variant {variant} seed {seed} {'in window' if scaled else 'raw'}"
+            note(label)
+            compare(run_onboard(torch_cuda, hip, obs, mission), oracle.onboard(obs, mission), label)
+
+
 @pytest.mark.parametrize("sweep", [False, True])
 def test_near_cancelling_cluster_sign(torch_cuda, hip, sweep):
     """Slalom clusters whose y centres nearly cancel: the float sum in scan
