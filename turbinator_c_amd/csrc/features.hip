@@ -253,6 +253,9 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
     // so that wave 0 reads them at 16-bit immediate offsets from one address
     // register; wave 0 turns positions into bin indices.
     __shared__ u32x2 dpart[DIAG ? 16 * kStagePitch : 1];
+    // DIAG: the environment's 432-byte diagnostics row, assembled here and
+    // written by wave 1 as 27 lane-consecutive 16-byte stores.
+    __shared__ u32x4 drow[DIAG ? kDiagBytes / 16 : 1];
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool has_cameras = DEPTH || rows.cameras != nullptr;
 
@@ -374,7 +377,7 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
             out[126 + w * 4 + lane] = 0.0f;
         }
         if constexpr (DIAG) {  // camera words are dead after this
-            unsigned char *diag = rows.diag + env * kDiagBytes;
+            unsigned char *diag = reinterpret_cast<unsigned char *>(drow);
             unsigned short *occ = reinterpret_cast<unsigned short *>(diag + kDiagCamOcc);
             if (has_cameras) {
                 const unsigned top_min = min_same_qx(bytes_min(px[1], bytes_min(px[0], 255u)));
@@ -443,13 +446,16 @@ __global__ __launch_bounds__(kBlockThreads) void features_kernel(Rows rows) {
                     best = take ? m : best;
                     first = take ? 4 * c + pos : first;
                 }
-                unsigned char *diag = rows.diag + env * kDiagBytes;
+                unsigned char *diag = reinterpret_cast<unsigned char *>(drow);
                 reinterpret_cast<float *>(diag)[lane] = first == 0u ? -1.0f : best;
-                // Two sectors' 16-bit words per 32-bit store (even lanes).
                 const unsigned word = ((first - 1u) & 0xffu) | (count << 8);
-                const unsigned pair = word | (__shfl_xor(word, 1) << 16);
-                if ((lane & 1) == 0)
-                    reinterpret_cast<unsigned *>(diag + kDiagArgCount)[lane >> 1] = pair;
+                reinterpret_cast<unsigned short *>(diag + kDiagArgCount)[lane] = (unsigned short)word;
+                // The row is written by this wave only from here on.
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (lane < kDiagBytes / 16)
+                    reinterpret_cast<u32x4 *>(rows.diag + env * kDiagBytes)[lane] = drow[lane];
             }
         // The stage is reused by this block's next environment, if any.
         if (env + gridDim.x < rows.batch) __syncthreads();
