@@ -18,16 +18,21 @@
 //     The closest return is a 32-bit wave minimum of the range bits followed
 //     by a lane-mask search for its first slot and lane (the first minimum
 //     in the reference scan order); the corridor minimum is a DPP / permlane
-//     fminf reduction; the cluster count comes from lane masks, and the
-//     cluster's y centres are added in float in ray order, as the reference
-//     does, because the sign of that sum picks the slalom lane;
+//     fminf reduction, with a +0 / -0 tie settled as the reference's strict
+//     < settles it (the first in ray order); the cluster count comes from
+//     lane masks, and the cluster's y centres are added in float in ray
+//     order, as the reference does, because the sign of that sum picks the
+//     slalom lane;
 //   * the tactical features and the controller (mission decode, targets,
 //     landing / standard / inversion / BWB laws, cannon) run in a second
 //     kernel from the parked scan results: one lane per environment for the
 //     tactical features, one quad of lanes per environment for the
 //     controller (lane a evaluates arm a and a quarter of the independent
 //     transcendental calls).  The controller's long register-heavy chain is
-//     kept apart from the scan so both keep their occupancy.
+//     kept apart from the scan so both keep their occupancy.  The angles
+//     that reach its angle wraps use a correctly rounded atan2: exact angles
+//     (from equal or zero components) reach a wrap's discontinuity, where
+//     one ulp flips the wrapped error's sign.
 //
 // Ray directions come from a table generated at build time with the host
 // libm (gen_ray_table.c), and the scan arithmetic is evaluated without FMA
