@@ -147,7 +147,11 @@ int tb_hip_actor_inputs_device(const float *obs, const float *mission,
  * w1[hidden][hidden], b1[hidden], w2[30][hidden], b2[30].  They are packed
  * once per weight update into a device buffer of
  * tb_hip_sac_actor_packed_bytes(hidden) bytes (16-byte aligned), which the
- * act entry reads; packed_bytes returns 0 for a hidden width out of range. */
+ * act entry reads; packed_bytes returns 0 for a hidden width out of range.
+ * The buffer holds each weight as three bf16 pieces whose sum is the weight
+ * exactly, for the bf16 matrix cores; a weight of magnitude >= 0x1.ffp127
+ * (or infinite) has no such split and makes the outputs it feeds NaN.
+ * Features of that magnitude are exact (their products are added in fp32). */
 size_t tb_hip_sac_actor_packed_bytes(int hidden);
 int tb_hip_sac_actor_pack_device(const float *w0, const float *b0, const float *w1,
                                  const float *b1, const float *w2, const float *b2,

@@ -7,22 +7,49 @@
 //   tb_actor_sample  training.c:306-329  clamped log-std, tanh-squashed
 //                                        Gaussian action, log-probability
 //
-// The three dense layers run on the matrix cores (v_mfma_f32_16x16x4f32,
-// fp32 in and out) as transposed products  H^T = W * X^T  over groups of 16
+// The three dense layers run on the bf16 matrix cores
+// (v_mfma_f32_16x16x32_bf16) with fp32 operands split exactly into three
+// bf16 pieces, x = hi + mid + lo:
+//   hi = bf16(x), mid = bf16(x - hi), lo = x - hi - mid,
+// each rounded to nearest even.  Both subtractions are exact (Sterbenz) and
+// the last residual has at most 8 significant bits, so lo holds it exactly.
+// A product is summed as the six cross terms whose pieces are not both
+// small: hi·hi, hi·mid, mid·hi, mid·mid, hi·lo and lo·hi (the "bf16x6" form
+// of Henry, Tang & Heinecke, "Leveraging the bfloat16 artificial
+// intelligence datatype for higher-precision computations", ARITH 2019).
+// The three dropped terms are at most 2^-23 |w x| together (|mid| <= 2^-9
+// |x|, |lo| <= 2^-17 |x|), below fp32's own rounding of the product, and
+// every cross product of two bf16 values is exact in the fp32 accumulator.
+// Six bf16 steps cost 3/8 of the fp32 matrix-core time of the same product.
+//
+// The products are transposed, H^T = W * X^T, over groups of 16
 // environments: the weights are the A operand and the environments the
-// columns of B.  With that orientation the 16x16 output fragment a lane
-// holds (outputs 16t+4g..16t+4g+3 of environment lane%16, g = lane/16) is
-// exactly the B-operand fragment of input chunk t of the next layer.  A
-// workgroup's four waves split every layer's output tiles between them and
-// pass the finished tiles to each other through LDS in that fragment layout.
+// columns of B.  The 16x16 output fragment a lane holds (outputs
+// 16t+4g..16t+4g+3 of environment lane%16, g = lane/16) is split and written
+// to LDS as the next layer's B operand: a 32-input chunk c holds hidden
+// tiles 2c and 2c+1, position 8g + 4h + v of the chunk being output
+// 16(2c+h) + 4g + v, so a lane's four outputs of tile 2c+h land in its own
+// 8-byte slot.  A workgroup's four waves split every layer's output tiles
+// between them and pass the finished tiles to each other through LDS.
 //
 // Weights are first packed (tb_hip_sac_actor_pack_device) into that operand
-// order: for output tile nt, input chunk s (16 inputs) and lane l, one float4
-// holds W[16nt + l%16][16s + 4(l/16) + 0..3], so every weight load of a wave
-// is one contiguous 1 KiB read.  Padding rows / columns hold zeros.  The
-// last layer's rows are interleaved (mean, log-std, mean, ...), so a lane's
-// output fragment holds two whole actions and the sampling runs on it in
-// registers.
+// order: for output tile nt, input chunk c, piece p and lane l, one 16-byte
+// vector holds the piece of W[16nt + l%16][k] for the eight chunk positions
+// 8(l/16) .. +7, so every weight load of a wave is one contiguous 1 KiB
+// read.  Padding rows / columns hold zeros.  The last layer's rows are
+// interleaved (mean, log-std, mean, ...), so a lane's output fragment holds
+// two whole actions and the sampling runs on it in registers.
+//
+// Inputs the split cannot carry.  An infinite feature, or one of magnitude
+// >= 0x1.ffp127 (which rounds to an infinite bf16), would multiply its zero
+// pieces into NaN.  Such a feature is zeroed in the split operand and its
+// exact product x * W[n][k] is added to the output by the lanes of its
+// environment, from an fp32 copy of the first layer's weights kept in the
+// packed buffer; an infinite input then gives the reference's +-inf (or NaN
+// where the reference's sum is NaN).  NaN inputs need nothing: every piece
+// of a NaN is NaN.  Weights are packed the same way but have no exact path:
+// a weight of magnitude >= 0x1.ffp127 is packed as NaN, so every output it
+// touches is NaN where the reference's would be infinite or saturated.
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -33,36 +60,48 @@
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kFeatures = 142;
 constexpr int kActions = 15;
 constexpr int kRaw = 2 * kActions;
-constexpr int kFeatureChunks = 9;  // 142 inputs padded to 144
+constexpr int kFeatureChunks = 5;  // 142 inputs padded to 160 = 5 chunks of 32
+constexpr int kPieces = 3;         // hi, mid, lo
+constexpr int kChunkBytes = 64;    // one piece of one 32-input chunk (32 bf16)
+constexpr int kBlockBytes = kPieces * 1024;  // one (tile, chunk) of a packed layer
 constexpr int kMinHidden = 16, kMaxHidden = 256;
 constexpr float kPi = 3.14159265358979323846f;
 constexpr size_t kMaxBatch = 0x7fffffffu;
 
-// Float offsets of the packed sections; every section starts on 256 bytes.
+// Byte offsets of the packed sections; every section starts on 256 bytes.
 struct Packed {
-    int ht;                 // hidden tiles (hidden padded to 16)
-    size_t w[3], b[3];      // section offsets (floats)
-    size_t total;           // floats
+    int ht, hc;             // hidden tiles (16 outputs), hidden chunks (32 inputs)
+    size_t w[3], b[3];      // weight pieces, fp32 biases
+    size_t w0;              // fp32 copy of the first layer's weights, [hidden][142]
+    size_t total;
 };
 
-__host__ __device__ inline size_t align64(size_t x) { return (x + 63) & ~(size_t)63; }
+__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 __host__ __device__ inline Packed packed_layout(int hidden) {
     Packed p;
     p.ht = (hidden + 15) / 16;
-    const int kc[3] = {kFeatureChunks, p.ht, p.ht};
+    p.hc = (p.ht + 1) / 2;
+    const int kc[3] = {kFeatureChunks, p.hc, p.hc};
     const int nt[3] = {p.ht, p.ht, 2};
     size_t off = 0;
     for (int l = 0; l < 3; ++l) {
         p.w[l] = off;
-        off = align64(off + (size_t)nt[l] * kc[l] * 256);
+        off = align256(off + (size_t)nt[l] * kc[l] * kBlockBytes);
         p.b[l] = off;
-        off = align64(off + (size_t)nt[l] * 16);
+        off = align256(off + (size_t)nt[l] * 16 * sizeof(float));
     }
+    p.w0 = off;
+    off = align256(off + (size_t)hidden * kFeatures * sizeof(float));
     p.total = off;
     return p;
 }
@@ -73,44 +112,91 @@ __host__ __device__ inline Packed packed_layout(int hidden) {
 // log-std) pairs of two consecutive actions.
 __host__ __device__ inline int raw_row(int p) { return (p & 1) ? kActions + (p >> 1) : (p >> 1); }
 
+// The layer input that chunk c, position s (0..31) of layer `layer` carries:
+// the features in order for the first layer; for the hidden layers the
+// position order of the tile exchange (position 8g + 4h + v of chunk c is
+// output 16(2c + h) + 4g + v of the previous layer).
+__host__ __device__ inline int chunk_input(int layer, int c, int s) {
+    if (layer == 0) return 32 * c + s;
+    const int g = s >> 3, i = s & 7;
+    return 16 * (2 * c + (i >> 2)) + 4 * g + (i & 3);
+}
+
+// Magnitudes from 0x1.ffp127 (0x7f7f8000) to infinity round to an infinite
+// bf16: the split cannot carry them.
+__device__ __forceinline__ bool unsplittable(float x) {
+    return (__float_as_uint(x) & 0x7fffffffu) - 0x7f7f8000u <= 0x8000u;
+}
+
+// The split of two values, as packed bf16 pairs per piece.
+__device__ __forceinline__ void split_pair(f32x2 x, unsigned &hi, unsigned &mid, unsigned &lo) {
+    hi = __builtin_bit_cast(unsigned, __builtin_convertvector(x, bf16x2));
+    const f32x2 hf = {__uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
+    const f32x2 r1 = {x[0] - hf[0], x[1] - hf[1]};
+    mid = __builtin_bit_cast(unsigned, __builtin_convertvector(r1, bf16x2));
+    const f32x2 mf = {__uint_as_float(mid << 16), __uint_as_float(mid & 0xffff0000u)};
+    const f32x2 r2 = {r1[0] - mf[0], r1[1] - mf[1]};
+    lo = __builtin_bit_cast(unsigned, __builtin_convertvector(r2, bf16x2));
+}
+
 struct PackArgs {
     const float *w[3], *b[3];
     int k[3], n[3], kc[3], nt[3];
+    int hidden;
     Packed layout;
-    float *out;
+    unsigned *out;  // the packed buffer as 32-bit words
 };
 
-// One thread per packed float.
+// The packed weight piece pair at byte offset `e` of layer l's weight
+// section: two bf16 values of one piece, chunk positions i0 and i0 + 1.
+__device__ unsigned packed_weight_pair(const PackArgs &a, int l, size_t e) {
+    const size_t block = e / kBlockBytes;
+    const int within = (int)(e % kBlockBytes);
+    const int piece = within / 1024, lane = (within % 1024) / 16, i0 = (within % 16) / 2;
+    const int tile = (int)(block / a.kc[l]), c = (int)(block % a.kc[l]);
+    const int n = 16 * tile + (lane & 15);
+    f32x2 v = {0.0f, 0.0f};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int k = chunk_input(l, c, 8 * (lane >> 4) + i0 + h);
+        if (n < a.n[l] && k < a.k[l]) {
+            v[h] = a.w[l][(size_t)(l == 2 ? raw_row(n) : n) * a.k[l] + k];
+            // No exact path for an unsplittable weight: NaN marks the outputs.
+            if (unsplittable(v[h])) v[h] = __builtin_nanf("");
+        }
+    }
+    unsigned p[kPieces];
+    split_pair(v, p[0], p[1], p[2]);
+    return p[piece];
+}
+
+// One thread per packed 32-bit word.
 __global__ __launch_bounds__(256) void sac_pack_kernel(PackArgs a) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.layout.total;
+    const size_t words = a.layout.total / 4;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < words;
          i += (size_t)gridDim.x * blockDim.x) {
-        float v = 0.0f;
+        const size_t byte = 4 * i;
+        unsigned v = 0;
         for (int l = 0; l < 3; ++l) {
-            const size_t wsize = (size_t)a.nt[l] * a.kc[l] * 256;
-            if (i >= a.layout.w[l] && i < a.layout.w[l] + wsize) {
-                const size_t e = i - a.layout.w[l];
-                const int t = (int)(e & 3);
-                const size_t q = e >> 2;
-                const int lane = (int)(q & 63);
-                const int s = (int)((q >> 6) % a.kc[l]);
-                const int tile = (int)((q >> 6) / a.kc[l]);
-                const int n = 16 * tile + (lane & 15);
-                const int k = 16 * s + 4 * (lane >> 4) + t;
-                if (n < a.n[l] && k < a.k[l])
-                    v = a.w[l][(size_t)(l == 2 ? raw_row(n) : n) * a.k[l] + k];
-            } else if (i >= a.layout.b[l] && i < a.layout.b[l] + (size_t)a.nt[l] * 16) {
-                const int e = (int)(i - a.layout.b[l]);
-                if (e < a.n[l]) v = a.b[l][l == 2 ? raw_row(e) : e];
+            const size_t wsize = (size_t)a.nt[l] * a.kc[l] * kBlockBytes;
+            if (byte >= a.layout.w[l] && byte < a.layout.w[l] + wsize) {
+                v = packed_weight_pair(a, l, byte - a.layout.w[l]);
+            } else if (byte >= a.layout.b[l] && byte < a.layout.b[l] + (size_t)a.nt[l] * 64) {
+                const int e = (int)((byte - a.layout.b[l]) / 4);
+                if (e < a.n[l]) v = __float_as_uint(a.b[l][l == 2 ? raw_row(e) : e]);
             }
         }
+        if (byte >= a.layout.w0 && byte < a.layout.w0 + (size_t)a.hidden * kFeatures * 4)
+            v = __float_as_uint(a.w[0][(byte - a.layout.w0) / 4]);
         a.out[i] = v;
     }
 }
 
 struct ActArgs {
-    const float *packed;
+    const void *packed;
     unsigned packed_bytes;
-    unsigned w_off[3], b_off[3];  // section offsets in bytes
+    unsigned w_off[3], b_off[3], w0_off;  // section offsets in bytes
+    int hidden;
     const float *features, *normals;
     float *actions, *log_prob, *raw;
     size_t batch;
@@ -145,30 +231,37 @@ __device__ __forceinline__ float tanh_hidden(float x) {
 constexpr int kWaves = 4;
 constexpr int kGroups = 2;  // groups of 16 environments per workgroup pass
 
+// LDS rows of the workgroup: one per environment, KC chunks of 192 bytes
+// (the hi, mid and lo pieces of 32 inputs, 64 bytes each), plus 16 bytes so
+// that the rows of a 16-byte read start on different banks.
+__host__ __device__ constexpr int row_bytes(int kc) { return kc * kPieces * kChunkBytes + 16; }
+
 // This wave's tiles nt = w + 4j (j < TPW, nt < NT) of one dense layer over
 // KC input chunks, for the workgroup's G groups of 16 environments:
-// out tile = W[tile] * in^T + b.  The layer's input rows are in LDS (`rows`,
-// S floats per environment): lane l reads the B-operand fragment of chunk s,
-// inputs 16s + 4g .. +3 of environment l % 16 of each group, as one float4.
-// Every weight fragment a wave loads feeds 4 G matrix-core steps, one per
-// group, so L2 delivers 1 KiB of weights per 4 G MFMAs.  Weight chunks
-// stream through a ring of kDepth register slots: the chunk of step
-// s + kDepth - 1 is requested while step s runs.  The loop has no branches:
-// a slot j past the layer's tiles (when NT is not a multiple of 4) reads its
-// weights and bias at an offset past the buffer end, which the buffer
-// resource returns as zeros, computes a zero tile and is never stored.  The
-// scheduling barrier keeps the compiler from hoisting every load of the
-// layer.  The per-tile accumulation order (chunk s outer, k-step t inner)
-// does not depend on how tiles or environments are spread over waves.
-constexpr int kDepth = 4;
+// out tile = W[tile] * in^T + b.  Lane l reads the B-operand fragment of
+// chunk s, pieces of positions 8g .. +7 of environment l % 16 of each group,
+// as three 16-byte LDS reads.  Every weight fragment a wave loads feeds
+// 6 G matrix-core steps, so L2 delivers 3 KiB of weights per 6 G MFMAs.
+// Weight chunks stream through a ring of kDepth register slots: the chunk
+// of step s + kDepth - 1 is requested while step s runs.  The loop has no
+// branches: a slot j past the layer's tiles (when NT is not a multiple of
+// 4) reads its weights and bias at an offset past the buffer end, which the
+// buffer resource returns as zeros, computes a zero tile and is never
+// stored except as the zero padding tile.  The scheduling barrier keeps the
+// compiler from hoisting every load of the layer.  The per-tile
+// accumulation order (chunk s outer, cross term inner) does not depend on
+// how tiles or environments are spread over waves.
 constexpr unsigned kPastEnd = 0x80000000u;  // lane offset beyond any packed buffer
 
-// The first kDepth - 1 weight chunks and the bias of this wave's tiles of one
-// layer, requested ahead of the layer (layer_prefetch) so that their round
-// trip overlaps the previous phase of the pass.
+template <int TPW>
+constexpr int ring_depth() { return TPW <= 2 ? 4 : 2; }
+
+// The first weight chunks and the bias of this wave's tiles of one layer,
+// requested ahead of the layer (layer_prefetch) so that their round trip
+// overlaps the previous phase of the pass.
 template <int TPW>
 struct LayerWeights {
-    f32x4 ring[kDepth][TPW];
+    u32x4 ring[ring_depth<TPW>()][TPW][kPieces];
     f32x4 bias[TPW];
 };
 
@@ -187,30 +280,55 @@ __device__ __forceinline__ void tile_slots(int w, int lane, unsigned (&wl)[TPW],
     }
 }
 
+template <int KC, int TPW>
+__device__ __forceinline__ void load_chunk(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
+                                           const unsigned (&wl)[TPW], const int (&nt)[TPW],
+                                           int s, u32x4 (&slot)[TPW][kPieces]) {
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p)
+            slot[j][p] = __builtin_amdgcn_raw_buffer_load_b128(
+                rsrc, wl[j], w_off + kBlockBytes * (nt[j] * KC + s) + 1024u * p, 0);
+}
+
 template <int KC, int NT, int TPW>
 __device__ __forceinline__ void layer_prefetch(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
                                                unsigned b_off, int w, int lane,
                                                LayerWeights<TPW> &lw) {
+    constexpr int D = ring_depth<TPW>();
     unsigned wl[TPW], bl[TPW];
     int nt[TPW];
     tile_slots<NT, TPW>(w, lane, wl, bl, nt);
 #pragma unroll
-    for (int j = 0; j < TPW; ++j) {
-        lw.bias[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, bl[j], b_off + 64u * nt[j], 0);
+    for (int j = 0; j < TPW; ++j)
+        lw.bias[j] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, bl[j], b_off + 64u * nt[j], 0));
 #pragma unroll
-        for (int d = 0; d < kDepth - 1; ++d)
-            if (d < KC)
-                lw.ring[d][j] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rsrc, wl[j], w_off + 1024u * (nt[j] * KC + d), 0);
-    }
+    for (int d = 0; d < D - 1; ++d)
+        if (d < KC) load_chunk<KC, TPW>(rsrc, w_off, wl, nt, d, lw.ring[d]);
 }
 
-template <int KC, int NT, int TPW, int G, bool TANH, int S>
+__device__ __forceinline__ f32x4 mfma_bf16(u32x4 w, u32x4 x, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w),
+                                                   __builtin_bit_cast(bf16x8, x), acc, 0, 0, 0);
+}
+
+// The six cross terms, small ones first: (weight piece, input piece).
+constexpr int kTermW[6] = {2, 0, 1, 1, 0, 0};
+constexpr int kTermX[6] = {0, 2, 1, 0, 1, 0};
+
+// Returns W * in^T + b for this wave's tiles (no activation).  `rows` are
+// the layer's input rows in LDS, RS bytes apart.
+template <int KC, int NT, int TPW, int G, int RS>
 __device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
-                                            const f32x4 *rows, LayerWeights<TPW> &lw,
+                                            const u32x4 *rows, LayerWeights<TPW> &lw,
                                             f32x4 (&out)[TPW][G], int w, int lane) {
+    constexpr int D = ring_depth<TPW>();
+    constexpr int RS16 = RS / 16;
     const int g = lane >> 4;
-    const f32x4 *in = rows + ((lane & 15) * S) / 4 + g;  // group q, chunk s: in[q 4S + 4 s]
+    const u32x4 *in = rows + (lane & 15) * RS16 + g;  // group q, chunk s, piece p:
+                                                      // in[16 q RS16 + 12 s + 4 p]
     unsigned wl[TPW], bl[TPW];
     int nt[TPW];
     tile_slots<NT, TPW>(w, lane, wl, bl, nt);
@@ -219,42 +337,40 @@ __device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigne
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
         for (int q = 0; q < G; ++q) acc[j][q] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4 xc[G], xn[G];
+    u32x4 xc[G][kPieces], xn[G][kPieces];
 #pragma unroll
-    for (int q = 0; q < G; ++q) xn[q] = xc[q] = in[q * 4 * S];
+    for (int q = 0; q < G; ++q)
+#pragma unroll
+        for (int p = 0; p < kPieces; ++p) xn[q][p] = xc[q][p] = in[16 * q * RS16 + 4 * p];
 #pragma unroll
     for (int s = 0; s < KC; ++s) {
-        if (s + kDepth - 1 < KC) {
-#pragma unroll
-            for (int j = 0; j < TPW; ++j)
-                lw.ring[(s + kDepth - 1) % kDepth][j] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rsrc, wl[j], w_off + 1024u * (nt[j] * KC + s + kDepth - 1), 0);
-        }
+        if (s + D - 1 < KC) load_chunk<KC, TPW>(rsrc, w_off, wl, nt, s + D - 1,
+                                                lw.ring[(s + D - 1) % D]);
         if (s + 1 < KC) {
 #pragma unroll
-            for (int q = 0; q < G; ++q) xn[q] = in[q * 4 * S + 4 * (s + 1)];
+            for (int q = 0; q < G; ++q)
+#pragma unroll
+                for (int p = 0; p < kPieces; ++p)
+                    xn[q][p] = in[16 * q * RS16 + 12 * (s + 1) + 4 * p];
         }
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+        for (int t = 0; t < 6; ++t)
 #pragma unroll
             for (int j = 0; j < TPW; ++j)
 #pragma unroll
                 for (int q = 0; q < G; ++q)
-                    acc[j][q] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                        lw.ring[s % kDepth][j][t], xc[q][t], acc[j][q], 0, 0, 0);
+                    acc[j][q] = mfma_bf16(lw.ring[s % D][j][kTermW[t]], xc[q][kTermX[t]],
+                                          acc[j][q]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int q = 0; q < G; ++q) xc[q] = xn[q];
+        for (int q = 0; q < G; ++q)
+#pragma unroll
+            for (int p = 0; p < kPieces; ++p) xc[q][p] = xn[q][p];
     }
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
-        for (int q = 0; q < G; ++q)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const float y = acc[j][q][v] + lw.bias[j][v];
-                out[j][q][v] = TANH ? tanh_hidden(y) : y;
-            }
+        for (int q = 0; q < G; ++q) out[j][q] = acc[j][q] + lw.bias[j];
 }
 
 __device__ __forceinline__ float finite_or_zero(float x) {  // training.c:61-63
@@ -264,19 +380,38 @@ __device__ __forceinline__ float clampf(float x, float lo, float hi) {  // train
     return x < lo ? lo : (x > hi ? hi : x);
 }
 
-// Writes this wave's hidden tiles into the workgroup's activation rows: lane
-// l holds outputs 16nt + 4g .. +3 of environment l % 16 of each group, which
-// is exactly the B-operand fragment of input chunk nt of the next layer.
-template <int TPW, int G, int NT, int S>
-__device__ __forceinline__ void store_tiles(f32x4 *rows, const f32x4 (&h)[TPW][G], int w,
+// Writes this wave's hidden tiles, after tanh, into the workgroup's
+// activation rows as split pieces: lane l's outputs 16nt + 4g .. +3 of
+// environment l % 16 go to chunk nt / 2, positions 8g + 4(nt % 2) .. +3.
+// NH is the number of tiles the next layer reads (the hidden tiles rounded
+// up to whole chunks): a slot past the hidden tiles computed a zero tile,
+// whose tanh is zero, and writes the padding.
+template <int TPW, int G, int NH, int RS>
+__device__ __forceinline__ void store_tiles(unsigned char *rows, f32x4 (&h)[TPW][G], int w,
                                             int lane) {
     const int g = lane >> 4, e = lane & 15;
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
         const int nt = w + kWaves * j;
-        if (nt < NT) {
+        if (nt < NH) {
 #pragma unroll
-            for (int q = 0; q < G; ++q) rows[((16 * q + e) * S) / 4 + 4 * nt + g] = h[j][q];
+            for (int q = 0; q < G; ++q) {
+                u32x2 pc[kPieces];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const f32x2 x = {tanh_hidden(h[j][q][2 * hh]), tanh_hidden(h[j][q][2 * hh + 1])};
+                    unsigned hi, mid, lo;
+                    split_pair(x, hi, mid, lo);
+                    pc[0][hh] = hi;
+                    pc[1][hh] = mid;
+                    pc[2][hh] = lo;
+                }
+                unsigned char *base = rows + (16 * q + e) * RS + (nt >> 1) * kPieces * kChunkBytes +
+                                      16 * g + 8 * (nt & 1);
+#pragma unroll
+                for (int p = 0; p < kPieces; ++p)
+                    *reinterpret_cast<u32x2 *>(base + kChunkBytes * p) = pc[p];
+            }
         }
     }
 }
@@ -284,33 +419,36 @@ __device__ __forceinline__ void store_tiles(f32x4 *rows, const f32x4 (&h)[TPW][G
 template <int HT, int G>
 __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
     constexpr int TPW = (HT + kWaves - 1) / kWaves;  // hidden tiles per wave
+    constexpr int HC = (HT + 1) / 2;                 // hidden chunks of 32 inputs
     static_assert(kWaves == 2 * G, "the hidden -> 30 layer gives each wave one (tile, group)");
     constexpr int E = 16 * G;                        // environments per workgroup pass
-    // Row stride of the workgroup's LDS rows (floats): the 144 padded
-    // features or the padded hidden activations, plus 4 so rows start on
-    // different banks.  Buffer 1 holds the features during layer 0 and the
-    // second hidden layer afterwards; buffer 0 the first hidden layer.
-    constexpr int S = (16 * HT > 16 * kFeatureChunks ? 16 * HT : 16 * kFeatureChunks) + 4;
-    __shared__ f32x4 buf[2][E * S / 4];
+    // Buffer 1 holds the features during layer 0 and the second hidden layer
+    // afterwards; buffer 0 the first hidden layer.
+    constexpr int RS = row_bytes(kFeatureChunks > HC ? kFeatureChunks : HC);
+    __shared__ u32x4 buf[2][E * RS / 16];
     __shared__ float term_s[E][16];
+    // Nonzero when the environment's feature row holds a value the split
+    // cannot carry (set while staging, cleared once layer 0 has read it).
+    __shared__ int special[E];
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, j = lane & 15;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.packed, a.packed_bytes);
+    if (tid < E) special[tid] = 0;
+    __syncthreads();
     // The loop bound is uniform over the block, so every wave meets the
     // barriers; rows past the batch end compute on zeros and store nothing.
     // Groups go to workgroups in XCD-contiguous order, the order in which the
     // feature kernel writes its rows, so that behind it a workgroup reads
-    // rows its own XCD wrote (14.9 -> 14.5 us at 16,384 rows).
+    // rows its own XCD wrote.
     for (size_t base = xcd_contiguous(blockIdx.x, gridDim.x) * E; base < a.batch;
          base += (size_t)gridDim.x * E) {
         // Stage the feature rows in buffer 1 (rows are 568 bytes, 8-byte
         // aligned): every 8-byte load of the pass is issued before any LDS
         // store, so the rows arrive in one round trip.  Rows past the batch
-        // end read as zero; inputs 142 and 143 are zero padding.
-        constexpr int kPairs = E * 72;  // 72 float pairs per padded row
+        // end read as zero; inputs 142 to 159 are zero padding.
+        constexpr int kPairs = E * 16 * kFeatureChunks;  // 80 float pairs per padded row
         constexpr int kPerThread = (kPairs + kWaves * 64 - 1) / (kWaves * 64);
-        typedef float f32x2 __attribute__((ext_vector_type(2)));
         f32x2 pairs[kPerThread];
         {
             const size_t rows = a.batch - base < (size_t)E ? a.batch - base : (size_t)E;
@@ -319,7 +457,7 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
 #pragma unroll
             for (int it = 0; it < kPerThread; ++it) {
                 const int q = tid + kWaves * 64 * it;
-                const int e = q / 72, k = 2 * (q - 72 * e);
+                const int e = q / 80, k = 2 * (q - 80 * e);
                 pairs[it] = (f32x2){0.0f, 0.0f};
                 if (q < kPairs && k < kFeatures)
                     pairs[it] = __builtin_bit_cast(
@@ -346,14 +484,23 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
                 drawn[h] = a.normals[env2 * kActions + act];
         }
         {
-            float *xs = reinterpret_cast<float *>(buf[1]);
+            unsigned char *xs = reinterpret_cast<unsigned char *>(buf[1]);
 #pragma unroll
             for (int it = 0; it < kPerThread; ++it) {
                 const int q = tid + kWaves * 64 * it;
-                const int e = q / 72, k = 2 * (q - 72 * e);
+                const int e = q / 80, k = 2 * (q - 80 * e);
                 if (q < kPairs) {
-                    xs[e * S + k] = pairs[it][0];
-                    xs[e * S + k + 1] = pairs[it][1];
+                    f32x2 x = pairs[it];
+                    const bool s0 = unsplittable(x[0]), s1 = unsplittable(x[1]);
+                    if (s0) x[0] = 0.0f;
+                    if (s1) x[1] = 0.0f;
+                    if (s0 || s1) special[e] = 1;
+                    unsigned pc[kPieces];
+                    split_pair(x, pc[0], pc[1], pc[2]);
+                    unsigned char *at = xs + e * RS + (k >> 5) * kPieces * kChunkBytes + 2 * (k & 31);
+#pragma unroll
+                    for (int p = 0; p < kPieces; ++p)
+                        *reinterpret_cast<unsigned *>(at + kChunkBytes * p) = pc[p];
                 }
             }
         }
@@ -364,24 +511,54 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
         LayerWeights<TPW> lw1;
         {
             f32x4 h[TPW][G];
-            layer_tiles<kFeatureChunks, HT, TPW, G, true, S>(wrs, a.w_off[0], buf[1], lw0, h, w,
-                                                             lane);
-            layer_prefetch<HT, HT, TPW>(wrs, a.w_off[1], a.b_off[1], w, lane, lw1);
-            store_tiles<TPW, G, HT, S>(buf[0], h, w, lane);
+            layer_tiles<kFeatureChunks, HT, TPW, G, RS>(wrs, a.w_off[0], buf[1], lw0, h, w, lane);
+            // The exact products of the unsplittable features, added by the
+            // lanes of their environment (rare: rows with +-inf or huge
+            // features).
+            bool mine[G];
+            bool any = false;
+#pragma unroll
+            for (int q = 0; q < G; ++q) {
+                mine[q] = special[16 * q + j] != 0;
+                any |= mine[q];
+            }
+            if (__builtin_amdgcn_ballot_w64(any)) {
+                const float *w0 = reinterpret_cast<const float *>(
+                    static_cast<const unsigned char *>(a.packed) + a.w0_off);
+#pragma unroll
+                for (int q = 0; q < G; ++q) {
+                    if (!mine[q]) continue;
+                    const float *row = a.features + (base + 16 * q + j) * kFeatures;
+                    for (int k = 0; k < kFeatures; ++k) {
+                        const float x = row[k];
+                        if (!unsplittable(x)) continue;
+#pragma unroll
+                        for (int jj = 0; jj < TPW; ++jj)
+#pragma unroll
+                            for (int v = 0; v < 4; ++v) {
+                                const int n = 16 * (w + kWaves * jj) + 4 * g + v;
+                                if (n < a.hidden) h[jj][q][v] += x * w0[(size_t)n * kFeatures + k];
+                            }
+                    }
+                }
+            }
+            layer_prefetch<HC, HT, TPW>(wrs, a.w_off[1], a.b_off[1], w, lane, lw1);
+            store_tiles<TPW, G, 2 * HC, RS>(reinterpret_cast<unsigned char *>(buf[0]), h, w, lane);
         }
         __syncthreads();
+        if (tid < E) special[tid] = 0;
         LayerWeights<1> lw2;
         {
             f32x4 h[TPW][G];
-            layer_tiles<HT, HT, TPW, G, true, S>(wrs, a.w_off[1], buf[0], lw1, h, w, lane);
-            layer_prefetch<HT, 2, 1>(wrs, a.w_off[2], a.b_off[2], tile2, lane, lw2);
-            store_tiles<TPW, G, HT, S>(buf[1], h, w, lane);
+            layer_tiles<HC, HT, TPW, G, RS>(wrs, a.w_off[1], buf[0], lw1, h, w, lane);
+            layer_prefetch<HC, 2, 1>(wrs, a.w_off[2], a.b_off[2], tile2, lane, lw2);
+            store_tiles<TPW, G, 2 * HC, RS>(reinterpret_cast<unsigned char *>(buf[1]), h, w, lane);
         }
         __syncthreads();
         {
             f32x4 r[1][1];
-            layer_tiles<HT, 2, 1, 1, false, S>(wrs, a.w_off[2], buf[1] + group2 * 4 * S, lw2, r,
-                                               tile2, lane);
+            layer_tiles<HC, 2, 1, 1, RS>(wrs, a.w_off[2], buf[1] + group2 * 16 * (RS / 16), lw2,
+                                         r, tile2, lane);
             // training.c:310-327 on this lane's two actions (the last lane
             // group of tile 1 holds one action and the padding).
             const bool live = env2 < a.batch;
@@ -425,7 +602,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 extern "C" size_t tb_hip_sac_actor_packed_bytes(int hidden) {
     if (hidden < kMinHidden || hidden > kMaxHidden) return 0;
-    return packed_layout(hidden).total * sizeof(float);
+    return packed_layout(hidden).total;
 }
 
 extern "C" int tb_hip_sac_actor_pack_device(const float *w0, const float *b0, const float *w1,
@@ -436,9 +613,10 @@ extern "C" int tb_hip_sac_actor_pack_device(const float *w0, const float *b0, co
         return 0;
     PackArgs a;
     a.layout = packed_layout(hidden);
+    a.hidden = hidden;
     const float *w[3] = {w0, w1, w2}, *b[3] = {b0, b1, b2};
     const int k[3] = {kFeatures, hidden, hidden}, n[3] = {hidden, hidden, kRaw};
-    const int kc[3] = {kFeatureChunks, a.layout.ht, a.layout.ht};
+    const int kc[3] = {kFeatureChunks, a.layout.hc, a.layout.hc};
     const int nt[3] = {a.layout.ht, a.layout.ht, 2};
     for (int l = 0; l < 3; ++l) {
         a.w[l] = w[l];
@@ -448,9 +626,9 @@ extern "C" int tb_hip_sac_actor_pack_device(const float *w0, const float *b0, co
         a.kc[l] = kc[l];
         a.nt[l] = nt[l];
     }
-    a.out = static_cast<float *>(packed);
+    a.out = static_cast<unsigned *>(packed);
     (void)hipGetLastError();
-    const size_t blocks = (a.layout.total + 255) / 256;
+    const size_t blocks = (a.layout.total / 4 + 255) / 256;
     sac_pack_kernel<<<(unsigned)blocks, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(a);
     return hipGetLastError() == hipSuccess;
 }
@@ -464,12 +642,14 @@ extern "C" int tb_hip_sac_actor_act_device(const void *packed, int hidden, const
         return 0;
     const Packed p = packed_layout(hidden);
     ActArgs a;
-    a.packed = static_cast<const float *>(packed);
-    a.packed_bytes = (unsigned)(p.total * sizeof(float));
+    a.packed = packed;
+    a.packed_bytes = (unsigned)p.total;
     for (int l = 0; l < 3; ++l) {
-        a.w_off[l] = (unsigned)(p.w[l] * sizeof(float));
-        a.b_off[l] = (unsigned)(p.b[l] * sizeof(float));
+        a.w_off[l] = (unsigned)p.w[l];
+        a.b_off[l] = (unsigned)p.b[l];
     }
+    a.w0_off = (unsigned)p.w0;
+    a.hidden = hidden;
     a.features = features;
     a.normals = normals;
     a.actions = actions;
