@@ -148,10 +148,10 @@ int tb_hip_actor_inputs_device(const float *obs, const float *mission,
  * once per weight update into a device buffer of
  * tb_hip_sac_actor_packed_bytes(hidden) bytes (16-byte aligned), which the
  * act entry reads; packed_bytes returns 0 for a hidden width out of range.
- * The buffer holds each weight as three bf16 pieces whose sum is the weight
- * exactly, for the bf16 matrix cores; a weight of magnitude >= 0x1.ffp127
- * (or infinite) has no such split and makes the outputs it feeds NaN.
- * Features of that magnitude are exact (their products are added in fp32). */
+ * The buffer holds each weight row scaled by a power of two and split into
+ * two fp16 pieces for the fp16 matrix cores (products within about 7e-7 of
+ * their fp32 value); weights must be finite: a non-finite weight makes its
+ * output NaN for every row, where the reference's would be +-inf or NaN. */
 size_t tb_hip_sac_actor_packed_bytes(int hidden);
 int tb_hip_sac_actor_pack_device(const float *w0, const float *b0, const float *w1,
                                  const float *b1, const float *w2, const float *b2,

@@ -3,8 +3,10 @@
 tb_sac_act_features bit for bit (tests/test_sac_actor_oracle.py).
 
 The matrix cores sum in another order than the reference's sequential loop,
-and tanhf / expf / logf are the device library's, so each output is held to
-a bound set by its own conditioning:
+each product is formed from exact three-piece bf16 splits of its operands
+with the three smallest cross terms (together at most 2^-23 of the product)
+left out, and tanhf / expf / logf are the device library's, so each output
+is held to a bound set by its own conditioning:
   * raw outputs: 1e-5 (1 + S), S = |b2| + sum_k |w2_k h1_k| the magnitude of
     the final layer's summands (float64, from the weights);
   * actions: (1 - a^2) dz + 2.4e-7, dz the raw bound of the mean plus the
@@ -130,6 +132,80 @@ def test_saturating_and_special_rows(torch_cuda, hip):
     got = run_gpu(torch_cuda, w, hidden, feats, draws)
     stats = check(got, oracle.sac_actor(ow, feats, draws), w, feats, draws, "saturating")
     note(f"saturating: {stats}")
+
+
+def f32_bits(u: int) -> np.float32:
+    return np.frombuffer(np.uint32(u).tobytes(), np.float32)[0]
+
+
+@pytest.mark.parametrize("hidden", [37, 128])
+def test_extreme_and_infinite_features(torch_cuda, hip, hidden):
+    """Features at the ends of the float range.  Finite ones go through the
+    split at a per-row scale; infinite ones have no split and the kernel adds
+    their products in fp32.  Rows: 0x1.ffp127 of each sign, FLT_MAX, -inf and
+    +inf in one row (per output +-inf or NaN, as the reference's sum falls),
+    two FLT_MAX, 0x1.ffp127 beside the largest float below it, a row of
+    -FLT_MAX / 64 only, and +inf in the last feature.  Every partial sum of
+    the reference's loop stays finite here: a row whose sequential sum
+    overflows partway (142 terms of FLT_MAX) ends at an infinity that depends
+    on the summation order, which no parallel sum reproduces."""
+    note(f"sac actor extreme features, hidden {hidden}")
+    w = random_weights(hidden, seed=5)
+    feats = random_features(64, seed=13)
+    big, below = f32_bits(0x7F7F8000), f32_bits(0x7F7F7FFF)
+    fmax = np.finfo(np.float32).max
+    feats[0, 0] = big
+    feats[1, 141] = -big
+    feats[2, 70] = fmax
+    feats[3, 3], feats[3, 9] = -np.inf, np.inf
+    feats[4, 10] = feats[4, 11] = fmax
+    feats[5, 20], feats[5, 21] = big, below
+    feats[6, :] = -fmax / 64
+    feats[7, 141] = np.inf
+    draws = np.random.default_rng(6).standard_normal((64, 15)).astype(np.float32)
+    ow = oracle.SacActorWeights(*w)
+    for d in (None, draws):
+        got = run_gpu(torch_cuda, w, hidden, feats, d)
+        want = oracle.sac_actor(ow, feats, d)
+        stats = check(got, want, w, feats, d, f"extreme h{hidden}")
+        note(f"extreme hidden {hidden} {'det' if d is None else 'stoch'}: {stats}")
+
+
+def wide_range_case(seed: int = 21):
+    """Operand rows across the float range, for the matrix cores' per-row
+    scaling: first-layer weight rows at scales 10^U(-15, 15) and feature
+    rows at 10^U(-15, 15), each with entries spread over 10^U(-10, 0) of
+    their row's scale; hidden-layer rows at their usual scale but spread over
+    10^U(-8, 0) (the low pieces of the smallest are fp16 subnormals at the
+    row's scale); an all-zero weight row per layer and an all-zero feature
+    row.  Products stay below 1e30, so the reference's sums stay finite.
+    Hidden-layer weights keep their usual scale because larger ones amplify
+    the hidden tanh's own rounding (about 2e-7 absolute here, an ulp in the
+    reference) past a bound on the last layer's sum."""
+    hidden = 128
+    rng = np.random.default_rng(seed)
+    w = random_weights(hidden, seed=seed)
+    for li, (lo, hi) in ((0, (-15, 15)), (2, (0, 0)), (4, (0, 0))):
+        rows = w[li].shape[0]
+        row_scale = 10.0 ** rng.uniform(lo, hi, (rows, 1))
+        spread = 10.0 ** rng.uniform(-10 if li == 0 else -8, 0, w[li].shape)
+        w[li] = (w[li] * row_scale * spread).astype(np.float32)
+        w[li][rows // 2] = 0.0
+    feats = (rng.choice([-1.0, 1.0], (256, 142)) * 10.0 ** rng.uniform(-15, 15, (256, 1))
+             * 10.0 ** rng.uniform(-10, 0, (256, 142))).astype(np.float32)
+    feats[7] = 0.0
+    return hidden, w, feats
+
+
+def test_wide_dynamic_range(torch_cuda, hip):
+    note("sac actor wide dynamic range, hidden 128")
+    hidden, w, feats = wide_range_case()
+    draws = np.random.default_rng(22).standard_normal((256, 15)).astype(np.float32)
+    ow = oracle.SacActorWeights(*w)
+    for d in (None, draws):
+        got = run_gpu(torch_cuda, w, hidden, feats, d)
+        stats = check(got, oracle.sac_actor(ow, feats, d), w, feats, d, "wide range")
+        note(f"wide range {'det' if d is None else 'stoch'}: {stats}")
 
 
 @pytest.mark.parametrize("batch", [1, 15, 63, 65, 16384])

@@ -143,15 +143,15 @@ def test_checkpoint_reader_rejects_bad_files(tmp_path):
 def test_packed_sizes():
     assert actor.packed_bytes(15) == 0 and actor.packed_bytes(257) == 0
     # hidden 128: 8 tiles of 16 outputs, 4 chunks of 32 inputs (5 for the 142
-    # features).  Per layer, 3 KiB of split weight pieces per (tile, chunk) and
-    # 64 bytes of fp32 bias per tile; then the fp32 first-layer weights; every
-    # section rounded up to 256 bytes.
+    # features).  Per layer, 2 KiB of fp16 weight pieces per (tile, chunk) and
+    # 128 bytes of fp32 biases and int exponents per tile; then the fp32
+    # first-layer weights; every section rounded up to 256 bytes.
     def up(x):
         return (x + 255) // 256 * 256
-    sections = [8 * 5 * 3072, 8 * 64, 8 * 4 * 3072, 8 * 64, 2 * 4 * 3072, 2 * 64, 128 * 142 * 4]
-    assert actor.packed_bytes(128) == sum(up(x) for x in sections) == 319744
-    # hidden 37: 3 tiles, 2 chunks; hidden 256: 16 tiles, 8 chunks.
-    assert actor.packed_bytes(37) == sum(up(x) for x in [
-        3 * 5 * 3072, 3 * 64, 3 * 2 * 3072, 3 * 64, 2 * 2 * 3072, 2 * 64, 37 * 142 * 4])
-    assert actor.packed_bytes(256) == sum(up(x) for x in [
-        16 * 5 * 3072, 16 * 64, 16 * 8 * 3072, 16 * 64, 2 * 8 * 3072, 2 * 64, 256 * 142 * 4])
+
+    def layout(ht, hc, hidden):
+        return [ht * 5 * 2048, ht * 128, ht * hc * 2048, ht * 128, 2 * hc * 2048, 2 * 128,
+                hidden * 142 * 4]
+    assert actor.packed_bytes(128) == sum(up(x) for x in layout(8, 4, 128)) == 238848
+    assert actor.packed_bytes(37) == sum(up(x) for x in layout(3, 2, 37))
+    assert actor.packed_bytes(256) == sum(up(x) for x in layout(16, 8, 256))

@@ -7,20 +7,28 @@
 //   tb_actor_sample  training.c:306-329  clamped log-std, tanh-squashed
 //                                        Gaussian action, log-probability
 //
-// The three dense layers run on the bf16 matrix cores
-// (v_mfma_f32_16x16x32_bf16) with fp32 operands split exactly into three
-// bf16 pieces, x = hi + mid + lo:
-//   hi = bf16(x), mid = bf16(x - hi), lo = x - hi - mid,
-// each rounded to nearest even.  Both subtractions are exact (Sterbenz) and
-// the last residual has at most 8 significant bits, so lo holds it exactly.
-// A product is summed as the six cross terms whose pieces are not both
-// small: hi·hi, hi·mid, mid·hi, mid·mid, hi·lo and lo·hi (the "bf16x6" form
-// of Henry, Tang & Heinecke, "Leveraging the bfloat16 artificial
-// intelligence datatype for higher-precision computations", ARITH 2019).
-// The three dropped terms are at most 2^-23 |w x| together (|mid| <= 2^-9
-// |x|, |lo| <= 2^-17 |x|), below fp32's own rounding of the product, and
-// every cross product of two bf16 values is exact in the fp32 accumulator.
-// Six bf16 steps cost 3/8 of the fp32 matrix-core time of the same product.
+// The three dense layers run on the fp16 matrix cores
+// (v_mfma_f32_16x16x32_f16) with each fp32 operand split into two fp16
+// pieces, x = hi + lo + err:  hi = fp16(x), lo = fp16(x - hi), both rounded
+// to nearest even.  The subtraction is exact (Sterbenz), so while lo is a
+// normal fp16, |err| <= 2^-22 |x|.  A product is summed as the three cross
+// terms hi·hi, hi·lo and lo·hi: the dropped lo·lo and the two operands'
+// errors come to at most 3·2^-22 |w x| (about 7e-7), and each cross product
+// of two fp16 values is exact in the fp32 accumulator.  Three fp16 steps
+// take 3/16 of the fp32 matrix-core time of the same product.  (The
+// two-piece fp16 split with three products is the scheme of Ootomo and
+// Yokota, "Recovering single precision accuracy from Tensor Cores while
+// surpassing the FP32 theoretical peak performance", IJHPCA 36(4), 2022;
+// the range handling below is this kernel's.)
+//
+// Range.  fp16 is normal from 2^-14 to 65504, so every operand row is
+// scaled by a power of two that brings its largest magnitude into
+// [2^14, 2^15): each weight row when it is packed, each environment's
+// features while they are staged, and the hidden activations (tanh, at
+// most 1) by 2^14.  A piece more than 2^28 below its row's largest
+// magnitude is an fp16 subnormal, whose rounding (at most 2^-25 at that
+// scale) is below 2^-39 of the row's largest magnitude.  The sums are
+// unscaled with ldexp before the bias is added (exact: powers of two).
 //
 // The products are transposed, H^T = W * X^T, over groups of 16
 // environments: the weights are the A operand and the environments the
@@ -34,22 +42,21 @@
 //
 // Weights are first packed (tb_hip_sac_actor_pack_device) into that operand
 // order: for output tile nt, input chunk c, piece p and lane l, one 16-byte
-// vector holds the piece of W[16nt + l%16][k] for the eight chunk positions
-// 8(l/16) .. +7, so every weight load of a wave is one contiguous 1 KiB
-// read.  Padding rows / columns hold zeros.  The last layer's rows are
+// vector holds the piece of the scaled W[16nt + l%16][k] for the eight
+// chunk positions 8(l/16) .. +7, so every weight load of a wave is one
+// contiguous 1 KiB read; each tile's biases and unscale exponents follow
+// its layer.  Padding rows / columns hold zeros.  The last layer's rows are
 // interleaved (mean, log-std, mean, ...), so a lane's output fragment holds
 // two whole actions and the sampling runs on it in registers.
 //
-// Inputs the split cannot carry.  An infinite feature, or one of magnitude
-// >= 0x1.ffp127 (which rounds to an infinite bf16), would multiply its zero
-// pieces into NaN.  Such a feature is zeroed in the split operand and its
-// exact product x * W[n][k] is added to the output by the lanes of its
-// environment, from an fp32 copy of the first layer's weights kept in the
-// packed buffer; an infinite input then gives the reference's +-inf (or NaN
-// where the reference's sum is NaN).  NaN inputs need nothing: every piece
-// of a NaN is NaN.  Weights are packed the same way but have no exact path:
-// a weight of magnitude >= 0x1.ffp127 is packed as NaN, so every output it
-// touches is NaN where the reference's would be infinite or saturated.
+// Infinite features have no split (their pieces would multiply zeros into
+// NaN).  Such a feature is zeroed in the split operand and its product
+// x * W[n][k] is added in fp32 by the lanes of its environment, from an
+// fp32 copy of the first layer's weights kept in the packed buffer, which
+// gives the reference's +-inf (or NaN where the reference's sum is NaN).
+// NaN inputs need nothing: both pieces of a NaN are NaN.  Weights have no
+// such path: a non-finite weight makes its row's output NaN for every
+// environment, where the reference's would be +-inf or NaN.
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -63,16 +70,19 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kFeatures = 142;
 constexpr int kActions = 15;
 constexpr int kRaw = 2 * kActions;
 constexpr int kFeatureChunks = 5;  // 142 inputs padded to 160 = 5 chunks of 32
-constexpr int kPieces = 3;         // hi, mid, lo
-constexpr int kChunkBytes = 64;    // one piece of one 32-input chunk (32 bf16)
+constexpr int kPieces = 2;         // hi, lo
+constexpr int kChunkBytes = 64;    // one piece of one 32-input chunk (32 fp16)
 constexpr int kBlockBytes = kPieces * 1024;  // one (tile, chunk) of a packed layer
+constexpr int kTileScaleBytes = 128;          // per tile: 16 fp32 biases, 16 int exponents
+constexpr int kHiddenScale = 14;              // tanh outputs enter a layer times 2^14
 constexpr int kMinHidden = 16, kMaxHidden = 256;
 constexpr float kPi = 3.14159265358979323846f;
 constexpr size_t kMaxBatch = 0x7fffffffu;
@@ -80,7 +90,7 @@ constexpr size_t kMaxBatch = 0x7fffffffu;
 // Byte offsets of the packed sections; every section starts on 256 bytes.
 struct Packed {
     int ht, hc;             // hidden tiles (16 outputs), hidden chunks (32 inputs)
-    size_t w[3], b[3];      // weight pieces, fp32 biases
+    size_t w[3], b[3];      // weight pieces; fp32 biases and unscale exponents
     size_t w0;              // fp32 copy of the first layer's weights, [hidden][142]
     size_t total;
 };
@@ -98,7 +108,7 @@ __host__ __device__ inline Packed packed_layout(int hidden) {
         p.w[l] = off;
         off = align256(off + (size_t)nt[l] * kc[l] * kBlockBytes);
         p.b[l] = off;
-        off = align256(off + (size_t)nt[l] * 16 * sizeof(float));
+        off = align256(off + (size_t)nt[l] * kTileScaleBytes);
     }
     p.w0 = off;
     off = align256(off + (size_t)hidden * kFeatures * sizeof(float));
@@ -122,21 +132,26 @@ __host__ __device__ inline int chunk_input(int layer, int c, int s) {
     return 16 * (2 * c + (i >> 2)) + 4 * g + (i & 3);
 }
 
-// Magnitudes from 0x1.ffp127 (0x7f7f8000) to infinity round to an infinite
-// bf16: the split cannot carry them.
-__device__ __forceinline__ bool unsplittable(float x) {
-    return (__float_as_uint(x) & 0x7fffffffu) - 0x7f7f8000u <= 0x8000u;
+__device__ __forceinline__ bool infinite(float x) {
+    return (__float_as_uint(x) & 0x7fffffffu) == 0x7f800000u;
 }
 
-// The split of two values, as packed bf16 pairs per piece.
-__device__ __forceinline__ void split_pair(f32x2 x, unsigned &hi, unsigned &mid, unsigned &lo) {
-    hi = __builtin_bit_cast(unsigned, __builtin_convertvector(x, bf16x2));
-    const f32x2 hf = {__uint_as_float(hi << 16), __uint_as_float(hi & 0xffff0000u)};
-    const f32x2 r1 = {x[0] - hf[0], x[1] - hf[1]};
-    mid = __builtin_bit_cast(unsigned, __builtin_convertvector(r1, bf16x2));
-    const f32x2 mf = {__uint_as_float(mid << 16), __uint_as_float(mid & 0xffff0000u)};
-    const f32x2 r2 = {r1[0] - mf[0], r1[1] - mf[1]};
-    lo = __builtin_bit_cast(unsigned, __builtin_convertvector(r2, bf16x2));
+// The exponent t that brings a row whose largest magnitude has the bits
+// `max_bits` to [2^14, 2^15): 2^14 <= |max| 2^t < 2^15 for a normal max
+// (all zero or subnormal rows get t = 141; a NaN max gives -114, and the
+// row is NaN anyway).
+__host__ __device__ inline int row_exponent(unsigned max_bits) {
+    return 141 - (int)(max_bits >> 23);
+}
+
+// The split of two scaled values (|x| < 2^15), as packed fp16 pairs per
+// piece.
+__device__ __forceinline__ void split_pair(f32x2 x, unsigned &hi, unsigned &lo) {
+    const f16x2 h = __builtin_convertvector(x, f16x2);
+    const f32x2 hf = __builtin_convertvector(h, f32x2);
+    const f32x2 r = {x[0] - hf[0], x[1] - hf[1]};
+    hi = __builtin_bit_cast(unsigned, h);
+    lo = __builtin_bit_cast(unsigned, __builtin_convertvector(r, f16x2));
 }
 
 struct PackArgs {
@@ -147,26 +162,38 @@ struct PackArgs {
     unsigned *out;  // the packed buffer as 32-bit words
 };
 
+// The scale exponent of packed row n of layer l: the row's weights times
+// 2^s lie below 2^15 in magnitude.
+__device__ int row_scale(const PackArgs &a, int l, int n) {
+    if (n >= a.n[l]) return 0;
+    const float *row = a.w[l] + (size_t)(l == 2 ? raw_row(n) : n) * a.k[l];
+    unsigned m = 0;
+    for (int k = 0; k < a.k[l]; ++k) {
+        const unsigned b = __float_as_uint(row[k]) & 0x7fffffffu;
+        m = b > m ? b : m;
+    }
+    return row_exponent(m);
+}
+
 // The packed weight piece pair at byte offset `e` of layer l's weight
-// section: two bf16 values of one piece, chunk positions i0 and i0 + 1.
+// section: two fp16 values of one piece, chunk positions i0 and i0 + 1.
 __device__ unsigned packed_weight_pair(const PackArgs &a, int l, size_t e) {
     const size_t block = e / kBlockBytes;
     const int within = (int)(e % kBlockBytes);
     const int piece = within / 1024, lane = (within % 1024) / 16, i0 = (within % 16) / 2;
     const int tile = (int)(block / a.kc[l]), c = (int)(block % a.kc[l]);
     const int n = 16 * tile + (lane & 15);
+    const int scale = row_scale(a, l, n);
     f32x2 v = {0.0f, 0.0f};
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int k = chunk_input(l, c, 8 * (lane >> 4) + i0 + h);
-        if (n < a.n[l] && k < a.k[l]) {
-            v[h] = a.w[l][(size_t)(l == 2 ? raw_row(n) : n) * a.k[l] + k];
-            // No exact path for an unsplittable weight: NaN marks the outputs.
-            if (unsplittable(v[h])) v[h] = __builtin_nanf("");
-        }
+        if (n < a.n[l] && k < a.k[l])
+            v[h] = __builtin_amdgcn_ldexpf(
+                a.w[l][(size_t)(l == 2 ? raw_row(n) : n) * a.k[l] + k], scale);
     }
     unsigned p[kPieces];
-    split_pair(v, p[0], p[1], p[2]);
+    split_pair(v, p[0], p[1]);
     return p[piece];
 }
 
@@ -181,9 +208,18 @@ __global__ __launch_bounds__(256) void sac_pack_kernel(PackArgs a) {
             const size_t wsize = (size_t)a.nt[l] * a.kc[l] * kBlockBytes;
             if (byte >= a.layout.w[l] && byte < a.layout.w[l] + wsize) {
                 v = packed_weight_pair(a, l, byte - a.layout.w[l]);
-            } else if (byte >= a.layout.b[l] && byte < a.layout.b[l] + (size_t)a.nt[l] * 64) {
+            } else if (byte >= a.layout.b[l] &&
+                       byte < a.layout.b[l] + (size_t)a.nt[l] * kTileScaleBytes) {
+                // Tile block: biases of rows 16 t .. +15, then the exponents
+                // that undo the row scale (and the hidden inputs' 2^14).
                 const int e = (int)((byte - a.layout.b[l]) / 4);
-                if (e < a.n[l]) v = __float_as_uint(a.b[l][l == 2 ? raw_row(e) : e]);
+                const int n = 16 * (e / 32) + (e % 16);
+                if (n < a.n[l]) {
+                    if (e % 32 < 16)
+                        v = __float_as_uint(a.b[l][l == 2 ? raw_row(n) : n]);
+                    else
+                        v = (unsigned)(-row_scale(a, l, n) - (l == 0 ? 0 : kHiddenScale));
+                }
             }
         }
         if (byte >= a.layout.w0 && byte < a.layout.w0 + (size_t)a.hidden * kFeatures * 4)
@@ -216,9 +252,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, un
 // an ulp), infinities give +-1 and NaN stays NaN.  The next layer only sums
 // these values, so an absolute bound is what matters; the action's own tanh
 // uses the device library's tanhf.
-__device__ __forceinline__ float tanh_hidden(float x) {
+// Returned times 2^14, the scale at which hidden activations enter the
+// next layer (the same rounding: a power of two commutes with it).
+__device__ __forceinline__ float tanh_hidden_scaled(float x) {
     const float e = __builtin_amdgcn_exp2f(x * 2.88539008177792681f);  // 2 / ln 2
-    return __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+    return __builtin_fmaf(-32768.0f, __builtin_amdgcn_rcpf(e + 1.0f), 16384.0f);
 }
 
 // A workgroup's four waves share two groups of 16 environments: in the
@@ -231,19 +269,19 @@ __device__ __forceinline__ float tanh_hidden(float x) {
 constexpr int kWaves = 4;
 constexpr int kGroups = 2;  // groups of 16 environments per workgroup pass
 
-// LDS rows of the workgroup: one per environment, KC chunks of 192 bytes
-// (the hi, mid and lo pieces of 32 inputs, 64 bytes each), plus 16 bytes so
-// that the rows of a 16-byte read start on different banks.
+// LDS rows of the workgroup: one per environment, KC chunks of 128 bytes
+// (the hi and lo pieces of 32 inputs, 64 bytes each), plus 16 bytes so that
+// the rows of a 16-byte read start on different banks.
 __host__ __device__ constexpr int row_bytes(int kc) { return kc * kPieces * kChunkBytes + 16; }
 
 // This wave's tiles nt = w + 4j (j < TPW, nt < NT) of one dense layer over
 // KC input chunks, for the workgroup's G groups of 16 environments:
 // out tile = W[tile] * in^T + b.  Lane l reads the B-operand fragment of
 // chunk s, pieces of positions 8g .. +7 of environment l % 16 of each group,
-// as three 16-byte LDS reads.  Every weight fragment a wave loads feeds
-// 6 G matrix-core steps, so L2 delivers 3 KiB of weights per 6 G MFMAs.
-// Weight chunks stream through a ring of kDepth register slots: the chunk
-// of step s + kDepth - 1 is requested while step s runs.  The loop has no
+// as two 16-byte LDS reads.  Every weight fragment a wave loads feeds
+// 3 G matrix-core steps, so L2 delivers 2 KiB of weights per 3 G MFMAs.
+// Weight chunks stream through a ring of ring_depth register slots: the
+// chunk of step s + D - 1 is requested while step s runs.  The loop has no
 // branches: a slot j past the layer's tiles (when NT is not a multiple of
 // 4) reads its weights and bias at an offset past the buffer end, which the
 // buffer resource returns as zeros, computes a zero tile and is never
@@ -263,6 +301,7 @@ template <int TPW>
 struct LayerWeights {
     u32x4 ring[ring_depth<TPW>()][TPW][kPieces];
     f32x4 bias[TPW];
+    i32x4 unscale[TPW];
 };
 
 // Lane offsets of this wave's tile slots: a slot past the layer's NT tiles
@@ -275,7 +314,7 @@ __device__ __forceinline__ void tile_slots(int w, int lane, unsigned (&wl)[TPW],
         nt[j] = w + kWaves * j;
         const bool valid = nt[j] < NT;
         wl[j] = valid ? 16u * lane : kPastEnd;
-        bl[j] = valid ? 16u * (lane >> 4) : kPastEnd;
+        bl[j] = valid ? 16u * (lane >> 4) : kPastEnd;  // + 64 for the exponents
         if (!valid) nt[j] = 0;
     }
 }
@@ -301,34 +340,43 @@ __device__ __forceinline__ void layer_prefetch(__amdgpu_buffer_rsrc_t rsrc, unsi
     int nt[TPW];
     tile_slots<NT, TPW>(w, lane, wl, bl, nt);
 #pragma unroll
-    for (int j = 0; j < TPW; ++j)
+    for (int j = 0; j < TPW; ++j) {
         lw.bias[j] = __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, bl[j], b_off + 64u * nt[j], 0));
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, bl[j],
+                                                         b_off + kTileScaleBytes * nt[j], 0));
+        lw.unscale[j] = __builtin_bit_cast(
+            i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rsrc, bl[j], b_off + kTileScaleBytes * nt[j] + 64u, 0));
+    }
 #pragma unroll
     for (int d = 0; d < D - 1; ++d)
         if (d < KC) load_chunk<KC, TPW>(rsrc, w_off, wl, nt, d, lw.ring[d]);
 }
 
-__device__ __forceinline__ f32x4 mfma_bf16(u32x4 w, u32x4 x, f32x4 acc) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w),
-                                                   __builtin_bit_cast(bf16x8, x), acc, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 w, u32x4 x, f32x4 acc) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, w),
+                                                  __builtin_bit_cast(f16x8, x), acc, 0, 0, 0);
 }
 
-// The six cross terms, small ones first: (weight piece, input piece).
-constexpr int kTermW[6] = {2, 0, 1, 1, 0, 0};
-constexpr int kTermX[6] = {0, 2, 1, 0, 1, 0};
+// The three cross terms, small ones first: (weight piece, input piece).
+constexpr int kTerms = 3;
+constexpr int kTermW[kTerms] = {1, 0, 0};
+constexpr int kTermX[kTerms] = {0, 1, 0};
 
-// Returns W * in^T + b for this wave's tiles (no activation).  `rows` are
-// the layer's input rows in LDS, RS bytes apart.
+// Returns W * in^T + b for this wave's tiles (no activation): the scaled
+// sums times 2^(row exponent - shift[q]), plus the bias.  `rows` are the
+// layer's input rows in LDS, RS bytes apart; shift[q] is the scale exponent
+// of group q's inputs beyond the one the packed exponents already undo.
 template <int KC, int NT, int TPW, int G, int RS>
 __device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
                                             const u32x4 *rows, LayerWeights<TPW> &lw,
-                                            f32x4 (&out)[TPW][G], int w, int lane) {
+                                            const int (&shift)[G], f32x4 (&out)[TPW][G], int w,
+                                            int lane) {
     constexpr int D = ring_depth<TPW>();
     constexpr int RS16 = RS / 16;
     const int g = lane >> 4;
     const u32x4 *in = rows + (lane & 15) * RS16 + g;  // group q, chunk s, piece p:
-                                                      // in[16 q RS16 + 12 s + 4 p]
+                                                      // in[16 q RS16 + 8 s + 4 p]
     unsigned wl[TPW], bl[TPW];
     int nt[TPW];
     tile_slots<NT, TPW>(w, lane, wl, bl, nt);
@@ -351,16 +399,16 @@ __device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigne
             for (int q = 0; q < G; ++q)
 #pragma unroll
                 for (int p = 0; p < kPieces; ++p)
-                    xn[q][p] = in[16 * q * RS16 + 12 * (s + 1) + 4 * p];
+                    xn[q][p] = in[16 * q * RS16 + 8 * (s + 1) + 4 * p];
         }
 #pragma unroll
-        for (int t = 0; t < 6; ++t)
+        for (int t = 0; t < kTerms; ++t)
 #pragma unroll
             for (int j = 0; j < TPW; ++j)
 #pragma unroll
                 for (int q = 0; q < G; ++q)
-                    acc[j][q] = mfma_bf16(lw.ring[s % D][j][kTermW[t]], xc[q][kTermX[t]],
-                                          acc[j][q]);
+                    acc[j][q] = mfma_f16(lw.ring[s % D][j][kTermW[t]], xc[q][kTermX[t]],
+                                         acc[j][q]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int q = 0; q < G; ++q)
@@ -370,7 +418,11 @@ __device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigne
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
 #pragma unroll
-        for (int q = 0; q < G; ++q) out[j][q] = acc[j][q] + lw.bias[j];
+        for (int q = 0; q < G; ++q)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                out[j][q][v] = __builtin_amdgcn_ldexpf(acc[j][q][v], lw.unscale[j][v] - shift[q]) +
+                               lw.bias[j][v];
 }
 
 __device__ __forceinline__ float finite_or_zero(float x) {  // training.c:61-63
@@ -399,12 +451,12 @@ __device__ __forceinline__ void store_tiles(unsigned char *rows, f32x4 (&h)[TPW]
                 u32x2 pc[kPieces];
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
-                    const f32x2 x = {tanh_hidden(h[j][q][2 * hh]), tanh_hidden(h[j][q][2 * hh + 1])};
-                    unsigned hi, mid, lo;
-                    split_pair(x, hi, mid, lo);
+                    const f32x2 x = {tanh_hidden_scaled(h[j][q][2 * hh]),
+                                     tanh_hidden_scaled(h[j][q][2 * hh + 1])};
+                    unsigned hi, lo;
+                    split_pair(x, hi, lo);
                     pc[0][hh] = hi;
-                    pc[1][hh] = mid;
-                    pc[2][hh] = lo;
+                    pc[1][hh] = lo;
                 }
                 unsigned char *base = rows + (16 * q + e) * RS + (nt >> 1) * kPieces * kChunkBytes +
                                       16 * g + 8 * (nt & 1);
@@ -427,15 +479,16 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
     constexpr int RS = row_bytes(kFeatureChunks > HC ? kFeatureChunks : HC);
     __shared__ u32x4 buf[2][E * RS / 16];
     __shared__ float term_s[E][16];
-    // Nonzero when the environment's feature row holds a value the split
-    // cannot carry (set while staging, cleared once layer 0 has read it).
+    // Per environment of the pass: nonzero when its feature row holds an
+    // infinity, and the largest magnitude of its other features (as bits),
+    // both written while staging and read by layer 0.
     __shared__ int special[E];
+    __shared__ unsigned row_max[E];
     const int lane = threadIdx.x & 63, tid = threadIdx.x;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, j = lane & 15;
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.packed, a.packed_bytes);
-    if (tid < E) special[tid] = 0;
-    __syncthreads();
+
     // The loop bound is uniform over the block, so every wave meets the
     // barriers; rows past the batch end compute on zeros and store nothing.
     // Groups go to workgroups in XCD-contiguous order, the order in which the
@@ -444,25 +497,28 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
     for (size_t base = xcd_contiguous(blockIdx.x, gridDim.x) * E; base < a.batch;
          base += (size_t)gridDim.x * E) {
         // Stage the feature rows in buffer 1 (rows are 568 bytes, 8-byte
-        // aligned): every 8-byte load of the pass is issued before any LDS
-        // store, so the rows arrive in one round trip.  Rows past the batch
-        // end read as zero; inputs 142 to 159 are zero padding.
-        constexpr int kPairs = E * 16 * kFeatureChunks;  // 80 float pairs per padded row
-        constexpr int kPerThread = (kPairs + kWaves * 64 - 1) / (kWaves * 64);
-        f32x2 pairs[kPerThread];
+        // aligned): kRowThreads consecutive threads share an environment,
+        // each loading kRowPairs consecutive float pairs, every load of the
+        // pass issued before any LDS store so that the rows arrive in one
+        // round trip.  Rows past the batch end read as zero; inputs 142 to
+        // 159 are zero padding.
+        constexpr int kRowThreads = kWaves * 64 / E;             // 8
+        constexpr int kRowPairs = 16 * kFeatureChunks / kRowThreads;  // 10
+        static_assert(kRowThreads * kRowPairs == 16 * kFeatureChunks, "row split");
+        const int se = tid / kRowThreads, sr = tid % kRowThreads;
+        f32x2 pairs[kRowPairs];
         {
             const size_t rows = a.batch - base < (size_t)E ? a.batch - base : (size_t)E;
             const __amdgpu_buffer_rsrc_t frs =
                 make_rsrc(a.features + base * kFeatures, (unsigned)(rows * kFeatures * 4));
 #pragma unroll
-            for (int it = 0; it < kPerThread; ++it) {
-                const int q = tid + kWaves * 64 * it;
-                const int e = q / 80, k = 2 * (q - 80 * e);
+            for (int it = 0; it < kRowPairs; ++it) {
+                const int k = 2 * (kRowPairs * sr + it);
                 pairs[it] = (f32x2){0.0f, 0.0f};
-                if (q < kPairs && k < kFeatures)
+                if (k < kFeatures)
                     pairs[it] = __builtin_bit_cast(
                         f32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                                   frs, (unsigned)(e * kFeatures + k) * 4, 0, 0));
+                                   frs, (unsigned)(se * kFeatures + k) * 4, 0, 0));
             }
         }
         // Layer 0's first weight chunks and bias, requested with the
@@ -483,25 +539,48 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
             if (a.normals && act < kActions && env2 < a.batch)
                 drawn[h] = a.normals[env2 * kActions + act];
         }
+        // Infinite features go to the exact path (zero in the split operand);
+        // the row's largest other magnitude sets its scale.  The row's
+        // threads are kRowThreads consecutive lanes: both reduce by xor
+        // shuffles, and the first thread records them for layer 0.
         {
+            unsigned m = 0;
+            int inf = 0;
+#pragma unroll
+            for (int it = 0; it < kRowPairs; ++it) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    if (infinite(pairs[it][h])) {
+                        pairs[it][h] = 0.0f;
+                        inf = 1;
+                    }
+                    const unsigned b = __float_as_uint(pairs[it][h]) & 0x7fffffffu;
+                    m = b > m ? b : m;
+                }
+            }
+#pragma unroll
+            for (int d = 1; d < kRowThreads; d <<= 1) {
+                const unsigned o = (unsigned)__shfl_xor((int)m, d);
+                m = o > m ? o : m;
+                inf |= __shfl_xor(inf, d);
+            }
+            if (sr == 0) {
+                row_max[se] = m;
+                special[se] = inf;
+            }
+            const int t = row_exponent(m);
             unsigned char *xs = reinterpret_cast<unsigned char *>(buf[1]);
 #pragma unroll
-            for (int it = 0; it < kPerThread; ++it) {
-                const int q = tid + kWaves * 64 * it;
-                const int e = q / 80, k = 2 * (q - 80 * e);
-                if (q < kPairs) {
-                    f32x2 x = pairs[it];
-                    const bool s0 = unsplittable(x[0]), s1 = unsplittable(x[1]);
-                    if (s0) x[0] = 0.0f;
-                    if (s1) x[1] = 0.0f;
-                    if (s0 || s1) special[e] = 1;
-                    unsigned pc[kPieces];
-                    split_pair(x, pc[0], pc[1], pc[2]);
-                    unsigned char *at = xs + e * RS + (k >> 5) * kPieces * kChunkBytes + 2 * (k & 31);
+            for (int it = 0; it < kRowPairs; ++it) {
+                const int k = 2 * (kRowPairs * sr + it);
+                const f32x2 x = {__builtin_amdgcn_ldexpf(pairs[it][0], t),
+                                 __builtin_amdgcn_ldexpf(pairs[it][1], t)};
+                unsigned pc[kPieces];
+                split_pair(x, pc[0], pc[1]);
+                unsigned char *at = xs + se * RS + (k >> 5) * kPieces * kChunkBytes + 2 * (k & 31);
 #pragma unroll
-                    for (int p = 0; p < kPieces; ++p)
-                        *reinterpret_cast<unsigned *>(at + kChunkBytes * p) = pc[p];
-                }
+                for (int p = 0; p < kPieces; ++p)
+                    *reinterpret_cast<unsigned *>(at + kChunkBytes * p) = pc[p];
             }
         }
         __syncthreads();
@@ -511,10 +590,13 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
         LayerWeights<TPW> lw1;
         {
             f32x4 h[TPW][G];
-            layer_tiles<kFeatureChunks, HT, TPW, G, RS>(wrs, a.w_off[0], buf[1], lw0, h, w, lane);
-            // The exact products of the unsplittable features, added by the
-            // lanes of their environment (rare: rows with +-inf or huge
-            // features).
+            int shift[G];
+#pragma unroll
+            for (int q = 0; q < G; ++q) shift[q] = row_exponent(row_max[16 * q + j]);
+            layer_tiles<kFeatureChunks, HT, TPW, G, RS>(wrs, a.w_off[0], buf[1], lw0, shift, h, w,
+                                                        lane);
+            // The exact products of the infinite features, added by the
+            // lanes of their environment (rare).
             bool mine[G];
             bool any = false;
 #pragma unroll
@@ -531,7 +613,7 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
                     const float *row = a.features + (base + 16 * q + j) * kFeatures;
                     for (int k = 0; k < kFeatures; ++k) {
                         const float x = row[k];
-                        if (!unsplittable(x)) continue;
+                        if (!infinite(x)) continue;
 #pragma unroll
                         for (int jj = 0; jj < TPW; ++jj)
 #pragma unroll
@@ -546,19 +628,20 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
             store_tiles<TPW, G, 2 * HC, RS>(reinterpret_cast<unsigned char *>(buf[0]), h, w, lane);
         }
         __syncthreads();
-        if (tid < E) special[tid] = 0;
         LayerWeights<1> lw2;
         {
             f32x4 h[TPW][G];
-            layer_tiles<HC, HT, TPW, G, RS>(wrs, a.w_off[1], buf[0], lw1, h, w, lane);
+            int shift[G] = {};
+            layer_tiles<HC, HT, TPW, G, RS>(wrs, a.w_off[1], buf[0], lw1, shift, h, w, lane);
             layer_prefetch<HC, 2, 1>(wrs, a.w_off[2], a.b_off[2], tile2, lane, lw2);
             store_tiles<TPW, G, 2 * HC, RS>(reinterpret_cast<unsigned char *>(buf[1]), h, w, lane);
         }
         __syncthreads();
         {
             f32x4 r[1][1];
+            const int shift[1] = {0};
             layer_tiles<HC, 2, 1, 1, RS>(wrs, a.w_off[2], buf[1] + group2 * 16 * (RS / 16), lw2,
-                                         r, tile2, lane);
+                                         shift, r, tile2, lane);
             // training.c:310-327 on this lane's two actions (the last lane
             // group of tile 1 holds one action and the padding).
             const bool live = env2 < a.batch;
