@@ -9,7 +9,7 @@ guards the LDS stage between environments.  The caps:
     2^20 workgroups of one environment -> batches above 1,048,576;
   * actor plane kernel (tb_hip_actor_inputs_device): 2^20 workgroups of one
     environment -> above 1,048,576;
-  * compact SAC actor: 65,536 workgroups of 32 rows -> above 2,097,152 rows;
+  * compact SAC actor: 65,536 workgroups of 64 rows -> above 4,194,304 rows;
   * LiDAR transform: 2^20 workgroups of 256 values -> above 2^28 values.
   (The onboard controller's cap, 4,096 workgroups of 64 environments, is
   passed by the 263,144-row cases of test_gpu_onboard / test_gpu_actor_inputs.)
@@ -203,7 +203,7 @@ def test_actor_planes(torch_cuda, hip, planes):
 def test_sac_actor(torch_cuda, hip):
     torch = torch_cuda
     hidden, distinct = 128, 4096
-    batch = 65536 * 32 + distinct
+    batch = 65536 * 64 + distinct
     note(f"compact actor: {batch} rows tiled from {distinct}")
     rng = np.random.default_rng(2028)
     weights = []

@@ -37,7 +37,7 @@
 // to LDS as the next layer's B operand: a 32-input chunk c holds hidden
 // tiles 2c and 2c+1, position 8g + 4h + v of the chunk being output
 // 16(2c+h) + 4g + v, so a lane's four outputs of tile 2c+h land in its own
-// 8-byte slot.  A workgroup's four waves split every layer's output tiles
+// 8-byte slot.  A workgroup's eight waves split every layer's output tiles
 // between them and pass the finished tiles to each other through LDS.
 //
 // Weights are first packed (tb_hip_sac_actor_pack_device) into that operand
@@ -259,24 +259,29 @@ __device__ __forceinline__ float tanh_hidden_scaled(float x) {
     return __builtin_fmaf(-32768.0f, __builtin_amdgcn_rcpf(e + 1.0f), 16384.0f);
 }
 
-// A workgroup's four waves share two groups of 16 environments: in the
+// A workgroup's NW waves share NW / 2 groups of 16 environments: in the
 // 142 -> hidden and hidden -> hidden layers wave w computes output tiles
-// w, w + 4, w + 8, ... for both groups; in the hidden -> 30 layer (two tiles
-// per group) wave w computes tile w % 2 of group w / 2.  The finished tiles
-// go through LDS to all four waves as the next layer's input fragments.  A
-// 16,384-row batch is 512 workgroups, two per CU, so every SIMD holds two
-// waves with the same matrix-core work.  (Four groups per workgroup, one
-// workgroup and so one wave per SIMD, reads each weight once per CU instead
-// of twice but measured 11.7 against 9.6 us.)
-constexpr int kWaves = 4;
-constexpr int kGroups = 2;  // groups of 16 environments per workgroup pass
+// w, w + NW, ... for all groups; in the hidden -> 30 layer (two tiles per
+// group) wave w computes tile w % 2 of group w / 2.  The finished tiles go
+// through LDS to all the waves as the next layer's input fragments.  Above
+// 4 hidden tiles NW = 8: a 16,384-row batch is 256 workgroups, one per CU,
+// every SIMD holds two waves with the same matrix-core work, and a CU reads
+// each weight once (NW = 4, two workgroups per CU, reads each weight twice
+// per CU: 9.4 against 9.1 us at hidden 128; four groups on four waves, one
+// wave per SIMD: 11.7 us).  Up to 4 hidden tiles NW = 4, so that waves do
+// not compute empty tiles (hidden 16: 6.4 against 7.3 us).
+template <int HT>
+struct Shape {
+    static constexpr int waves = HT <= 4 ? 4 : 8;
+    static constexpr int groups = waves / 2;  // groups of 16 environments per workgroup pass
+};
 
 // LDS rows of the workgroup: one per environment, KC chunks of 128 bytes
 // (the hi and lo pieces of 32 inputs, 64 bytes each), plus 16 bytes so that
 // the rows of a 16-byte read start on different banks.
 __host__ __device__ constexpr int row_bytes(int kc) { return kc * kPieces * kChunkBytes + 16; }
 
-// This wave's tiles nt = w + 4j (j < TPW, nt < NT) of one dense layer over
+// This wave's tiles nt = w + NW j (j < TPW, nt < NT) of one dense layer over
 // KC input chunks, for the workgroup's G groups of 16 environments:
 // out tile = W[tile] * in^T + b.  Lane l reads the B-operand fragment of
 // chunk s, pieces of positions 8g .. +7 of environment l % 16 of each group,
@@ -285,7 +290,7 @@ __host__ __device__ constexpr int row_bytes(int kc) { return kc * kPieces * kChu
 // Weight chunks stream through a ring of ring_depth register slots: the
 // chunk of step s + D - 1 is requested while step s runs.  The loop has no
 // branches: a slot j past the layer's tiles (when NT is not a multiple of
-// 4) reads its weights and bias at an offset past the buffer end, which the
+// NW) reads its weights and bias at an offset past the buffer end, which the
 // buffer resource returns as zeros, computes a zero tile and is never
 // stored except as the zero padding tile.  The scheduling barrier keeps the
 // compiler from hoisting every load of the layer.  The per-tile
@@ -308,12 +313,12 @@ struct LayerWeights {
 
 // Lane offsets of this wave's tile slots: a slot past the layer's NT tiles
 // reads at kPastEnd (zeros through the buffer resource).
-template <int NT, int TPW>
+template <int NT, int TPW, int NW>
 __device__ __forceinline__ void tile_slots(int w, int lane, unsigned (&wl)[TPW],
                                            unsigned (&bl)[TPW], int (&nt)[TPW]) {
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
-        nt[j] = w + kWaves * j;
+        nt[j] = w + NW * j;
         const bool valid = nt[j] < NT;
         wl[j] = valid ? 16u * lane : kPastEnd;
         bl[j] = valid ? 16u * (lane >> 4) : kPastEnd;  // + 64 for the exponents
@@ -333,14 +338,14 @@ __device__ __forceinline__ void load_chunk(__amdgpu_buffer_rsrc_t rsrc, unsigned
                 rsrc, wl[j], w_off + kBlockBytes * (nt[j] * KC + s) + 1024u * p, 0);
 }
 
-template <int KC, int NT, int TPW>
+template <int KC, int NT, int TPW, int NW>
 __device__ __forceinline__ void layer_prefetch(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
                                                unsigned b_off, int w, int lane,
                                                LayerWeights<TPW> &lw) {
     constexpr int D = ring_depth<TPW>();
     unsigned wl[TPW], bl[TPW];
     int nt[TPW];
-    tile_slots<NT, TPW>(w, lane, wl, bl, nt);
+    tile_slots<NT, TPW, NW>(w, lane, wl, bl, nt);
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
         lw.bias[j] = __builtin_bit_cast(
@@ -369,7 +374,7 @@ constexpr int kTermX[kTerms] = {0, 1, 0};
 // sums times 2^(row exponent - shift[q]), plus the bias.  `rows` are the
 // layer's input rows in LDS, RS bytes apart; shift[q] is the scale exponent
 // of group q's inputs beyond the one the packed exponents already undo.
-template <int KC, int NT, int TPW, int G, int RS>
+template <int KC, int NT, int TPW, int G, int RS, int NW>
 __device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigned w_off,
                                             const u32x4 *rows, LayerWeights<TPW> &lw,
                                             const int (&shift)[G], f32x4 (&out)[TPW][G], int w,
@@ -381,7 +386,7 @@ __device__ __forceinline__ void layer_tiles(__amdgpu_buffer_rsrc_t rsrc, unsigne
                                                       // in[16 q RS16 + 8 s + 4 p]
     unsigned wl[TPW], bl[TPW];
     int nt[TPW];
-    tile_slots<NT, TPW>(w, lane, wl, bl, nt);
+    tile_slots<NT, TPW, NW>(w, lane, wl, bl, nt);
     f32x4 acc[TPW][G];
 #pragma unroll
     for (int j = 0; j < TPW; ++j)
@@ -440,13 +445,13 @@ __device__ __forceinline__ float clampf(float x, float lo, float hi) {  // train
 // NH is the number of tiles the next layer reads (the hidden tiles rounded
 // up to whole chunks): a slot past the hidden tiles computed a zero tile,
 // whose tanh is zero, and writes the padding.
-template <int TPW, int G, int NH, int RS>
+template <int TPW, int G, int NH, int RS, int NW>
 __device__ __forceinline__ void store_tiles(unsigned char *rows, f32x4 (&h)[TPW][G], int w,
                                             int lane) {
     const int g = lane >> 4, e = lane & 15;
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
-        const int nt = w + kWaves * j;
+        const int nt = w + NW * j;
         if (nt < NH) {
 #pragma unroll
             for (int q = 0; q < G; ++q) {
@@ -470,13 +475,13 @@ __device__ __forceinline__ void store_tiles(unsigned char *rows, f32x4 (&h)[TPW]
     }
 }
 
-template <int HT, int G>
-__global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
-    constexpr int TPW = (HT + kWaves - 1) / kWaves;  // hidden tiles per wave
+template <int HT, int G, int NW>
+__global__ __launch_bounds__(NW * 64) void sac_actor_kernel(ActArgs a) {
+    constexpr int TPW = (HT + NW - 1) / NW;  // hidden tiles per wave
     constexpr int HC = (HT + 1) / 2;                 // hidden chunks of 32 inputs
     // The hidden -> 30 layer's 2 G (tile, group) pairs, G2 groups per wave.
-    static_assert(2 * G % kWaves == 0, "whole groups per wave in the hidden -> 30 layer");
-    constexpr int G2 = 2 * G / kWaves;
+    static_assert(2 * G % NW == 0, "whole groups per wave in the hidden -> 30 layer");
+    constexpr int G2 = 2 * G / NW;
     constexpr int E = 16 * G;                        // environments per workgroup pass
     // Buffer 1 holds the features during layer 0 and the second hidden layer
     // afterwards; buffer 0 the first hidden layer.
@@ -506,7 +511,7 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
         // pass issued before any LDS store so that the rows arrive in one
         // round trip.  Rows past the batch end read as zero; inputs 142 to
         // 159 are zero padding.
-        constexpr int kRowThreads = kWaves * 64 / E;             // 8
+        constexpr int kRowThreads = NW * 64 / E;                 // 8
         constexpr int kRowPairs = 16 * kFeatureChunks / kRowThreads;  // 10
         static_assert(kRowThreads * kRowPairs == 16 * kFeatureChunks, "row split");
         const int se = tid / kRowThreads, sr = tid % kRowThreads;
@@ -528,7 +533,7 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
         // Layer 0's first weight chunks and bias, requested with the
         // features so that both round trips overlap.
         LayerWeights<TPW> lw0;
-        layer_prefetch<kFeatureChunks, HT, TPW>(wrs, a.w_off[0], a.b_off[0], w, lane, lw0);
+        layer_prefetch<kFeatureChunks, HT, TPW, NW>(wrs, a.w_off[0], a.b_off[0], w, lane, lw0);
         // The hidden -> 30 layer gives wave w tile w % 2 of the G2 groups
         // from group2 = G2 (w / 2) on: lane (g, j) then holds the (mean,
         // log-std) pairs of actions 8 (w % 2) + 2 g and + 1 of environment j
@@ -601,8 +606,8 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
             int shift[G];
 #pragma unroll
             for (int q = 0; q < G; ++q) shift[q] = row_exponent(row_max[16 * q + j]);
-            layer_tiles<kFeatureChunks, HT, TPW, G, RS>(wrs, a.w_off[0], buf[1], lw0, shift, h, w,
-                                                        lane);
+            layer_tiles<kFeatureChunks, HT, TPW, G, RS, NW>(wrs, a.w_off[0], buf[1], lw0, shift, h,
+                                                            w, lane);
             // The exact products of the infinite features, added by the
             // lanes of their environment (rare).
             bool mine[G];
@@ -626,29 +631,31 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
                         for (int jj = 0; jj < TPW; ++jj)
 #pragma unroll
                             for (int v = 0; v < 4; ++v) {
-                                const int n = 16 * (w + kWaves * jj) + 4 * g + v;
+                                const int n = 16 * (w + NW * jj) + 4 * g + v;
                                 if (n < a.hidden) h[jj][q][v] += x * w0[(size_t)n * kFeatures + k];
                             }
                     }
                 }
             }
-            layer_prefetch<HC, HT, TPW>(wrs, a.w_off[1], a.b_off[1], w, lane, lw1);
-            store_tiles<TPW, G, 2 * HC, RS>(reinterpret_cast<unsigned char *>(buf[0]), h, w, lane);
+            layer_prefetch<HC, HT, TPW, NW>(wrs, a.w_off[1], a.b_off[1], w, lane, lw1);
+            store_tiles<TPW, G, 2 * HC, RS, NW>(reinterpret_cast<unsigned char *>(buf[0]), h, w,
+                                                lane);
         }
         __syncthreads();
         LayerWeights<1> lw2;
         {
             f32x4 h[TPW][G];
             int shift[G] = {};
-            layer_tiles<HC, HT, TPW, G, RS>(wrs, a.w_off[1], buf[0], lw1, shift, h, w, lane);
-            layer_prefetch<HC, 2, 1>(wrs, a.w_off[2], a.b_off[2], tile2, lane, lw2);
-            store_tiles<TPW, G, 2 * HC, RS>(reinterpret_cast<unsigned char *>(buf[1]), h, w, lane);
+            layer_tiles<HC, HT, TPW, G, RS, NW>(wrs, a.w_off[1], buf[0], lw1, shift, h, w, lane);
+            layer_prefetch<HC, 2, 1, NW>(wrs, a.w_off[2], a.b_off[2], tile2, lane, lw2);
+            store_tiles<TPW, G, 2 * HC, RS, NW>(reinterpret_cast<unsigned char *>(buf[1]), h, w,
+                                                lane);
         }
         __syncthreads();
         {
             f32x4 r[1][G2];
             const int shift[G2] = {};
-            layer_tiles<HC, 2, 1, G2, RS>(wrs, a.w_off[2], buf[1] + group2 * 16 * (RS / 16), lw2,
+            layer_tiles<HC, 2, 1, G2, RS, NW>(wrs, a.w_off[2], buf[1] + group2 * 16 * (RS / 16), lw2,
                                           shift, r, tile2, lane);
             // training.c:310-327 on this lane's two actions of each group
             // (the last lane group of tile 1 holds one action and the
@@ -690,8 +697,11 @@ __global__ __launch_bounds__(kWaves * 64) void sac_actor_kernel(ActArgs a) {
 }
 
 template <int HT>
-void launch_act(const ActArgs &a, unsigned blocks, hipStream_t s) {
-    sac_actor_kernel<HT, kGroups><<<blocks, kWaves * 64, 0, s>>>(a);
+void launch_act(const ActArgs &a, hipStream_t s) {
+    constexpr int NW = Shape<HT>::waves, G = Shape<HT>::groups;
+    const size_t want = (a.batch + 16 * G - 1) / (16 * G);
+    const unsigned blocks = want > 65536 ? 65536u : (unsigned)want;
+    sac_actor_kernel<HT, G, NW><<<blocks, NW * 64, 0, s>>>(a);
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -754,27 +764,25 @@ extern "C" int tb_hip_sac_actor_act_device(const void *packed, int hidden, const
     a.log_prob = log_prob;
     a.raw = raw;
     a.batch = batch_size;
-    const size_t want = (batch_size + 16 * kGroups - 1) / (16 * kGroups);
-    const unsigned blocks = want > 65536 ? 65536u : (unsigned)want;
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     (void)hipGetLastError();
     switch (p.ht) {
-        case 1: launch_act<1>(a, blocks, s); break;
-        case 2: launch_act<2>(a, blocks, s); break;
-        case 3: launch_act<3>(a, blocks, s); break;
-        case 4: launch_act<4>(a, blocks, s); break;
-        case 5: launch_act<5>(a, blocks, s); break;
-        case 6: launch_act<6>(a, blocks, s); break;
-        case 7: launch_act<7>(a, blocks, s); break;
-        case 8: launch_act<8>(a, blocks, s); break;
-        case 9: launch_act<9>(a, blocks, s); break;
-        case 10: launch_act<10>(a, blocks, s); break;
-        case 11: launch_act<11>(a, blocks, s); break;
-        case 12: launch_act<12>(a, blocks, s); break;
-        case 13: launch_act<13>(a, blocks, s); break;
-        case 14: launch_act<14>(a, blocks, s); break;
-        case 15: launch_act<15>(a, blocks, s); break;
-        default: launch_act<16>(a, blocks, s); break;
+        case 1: launch_act<1>(a, s); break;
+        case 2: launch_act<2>(a, s); break;
+        case 3: launch_act<3>(a, s); break;
+        case 4: launch_act<4>(a, s); break;
+        case 5: launch_act<5>(a, s); break;
+        case 6: launch_act<6>(a, s); break;
+        case 7: launch_act<7>(a, s); break;
+        case 8: launch_act<8>(a, s); break;
+        case 9: launch_act<9>(a, s); break;
+        case 10: launch_act<10>(a, s); break;
+        case 11: launch_act<11>(a, s); break;
+        case 12: launch_act<12>(a, s); break;
+        case 13: launch_act<13>(a, s); break;
+        case 14: launch_act<14>(a, s); break;
+        case 15: launch_act<15>(a, s); break;
+        default: launch_act<16>(a, s); break;
     }
     return hipGetLastError() == hipSuccess;
 }
