@@ -104,7 +104,7 @@ def check(got, want, weights, feats, draws, label):
     return {"action_max": float(da.max()), "logp_max": float(dl.max())}
 
 
-@pytest.mark.parametrize("hidden", [16, 37, 128, 256])
+@pytest.mark.parametrize("hidden", [16, 37, 80, 128, 200, 256])
 def test_random_weights(torch_cuda, hip, hidden):
     note(f"sac actor hidden {hidden}, 1000 envs")
     w = random_weights(hidden, seed=hidden)
