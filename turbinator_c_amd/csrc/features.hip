@@ -484,20 +484,43 @@ int vector_bytes(const void *base, size_t stride, int widest) {
 }
 
 template <int LV, bool DIAG>
-void launch_lv(const Rows &rows, int cv, unsigned blocks, hipStream_t stream) {
+void launch_lv(const Rows &rows, int cv, unsigned blocks, unsigned lds, hipStream_t stream) {
     switch (cv) {
-    case 16: features_kernel<LV, 16, DIAG><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
-    case 8: features_kernel<LV, 8, DIAG><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
-    case 4: features_kernel<LV, 4, DIAG><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
-    default: features_kernel<LV, 1, DIAG><<<blocks, kBlockThreads, 0, stream>>>(rows); break;
+    case 16: features_kernel<LV, 16, DIAG><<<blocks, kBlockThreads, lds, stream>>>(rows); break;
+    case 8: features_kernel<LV, 8, DIAG><<<blocks, kBlockThreads, lds, stream>>>(rows); break;
+    case 4: features_kernel<LV, 4, DIAG><<<blocks, kBlockThreads, lds, stream>>>(rows); break;
+    default: features_kernel<LV, 1, DIAG><<<blocks, kBlockThreads, lds, stream>>>(rows); break;
     }
 }
 
 template <bool DIAG>
-void launch_diag(const Rows &rows, int lv, int cv, unsigned blocks, hipStream_t stream) {
-    if (lv == 4) launch_lv<4, DIAG>(rows, cv, blocks, stream);
-    else if (lv == 2) launch_lv<2, DIAG>(rows, cv, blocks, stream);
-    else launch_lv<1, DIAG>(rows, cv, blocks, stream);
+void launch_diag(const Rows &rows, int lv, int cv, unsigned blocks, unsigned lds,
+                 hipStream_t stream) {
+    if (lv == 4) launch_lv<4, DIAG>(rows, cv, blocks, lds, stream);
+    else if (lv == 2) launch_lv<2, DIAG>(rows, cv, blocks, lds, stream);
+    else launch_lv<1, DIAG>(rows, cv, blocks, lds, stream);
+}
+
+// Workgroups in flight per CU.  Its registers let the plain kernel hold 7
+// per CU; on the streaming layouts fewer keep HBM busier (16,384
+// environments, identical outputs): rows laid out as the reference's batch
+// 4 per CU (85.76 -> 83.99 us; 3 per CU 91.9 us), strided replay records 5
+// per CU (353.9 -> 348.1 us for 65,536 records).  Indexed gathers, fp32
+// depth cameras and the diagnostics variant keep their resource limit
+// (4 per CU measured 91.9 -> 94.8, 208.0 -> 210.3 and 94.2 -> 116.2 us).
+// The cap is dynamic LDS the kernel does not use: a workgroup then takes
+// more than 1 / (n + 1) of the CU's LDS, so n fit.
+constexpr unsigned kLdsPerCu = 160 * 1024;
+constexpr unsigned kStageLds = 16 * kStagePitch * sizeof(f32x4);
+
+unsigned occupancy_lds(const Rows &rows) {
+    if (rows.depth || rows.diag || rows.index) return 0;
+    const bool batch_rows = rows.obs_stride == kObsDim * sizeof(float) &&
+                            rows.mission_stride == 10 * sizeof(float) &&
+                            rows.camera_stride == 16384;
+    const unsigned per_cu = batch_rows ? 4 : 5;
+    const unsigned total = (kLdsPerCu / (per_cu + 1) + 1 + 1023) / 1024 * 1024;
+    return total - kStageLds;
 }
 
 template <int LV>
@@ -519,8 +542,8 @@ int launch_features(const Rows &rows, hipStream_t stream) {
         if (lv == 4) launch_depth<4>(rows, blocks, stream);
         else if (lv == 2) launch_depth<2>(rows, blocks, stream);
         else launch_depth<1>(rows, blocks, stream);
-    } else if (rows.diag) launch_diag<true>(rows, lv, cv, blocks, stream);
-    else launch_diag<false>(rows, lv, cv, blocks, stream);
+    } else if (rows.diag) launch_diag<true>(rows, lv, cv, blocks, 0, stream);
+    else launch_diag<false>(rows, lv, cv, blocks, occupancy_lds(rows), stream);
     return hipGetLastError() == hipSuccess;
 }
 
