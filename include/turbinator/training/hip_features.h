@@ -95,6 +95,24 @@ int tb_hip_extract_features_depth_device(const float *obs, const float *mission,
                                          const float *depth, float *features,
                                          size_t batch_size, void *stream);
 
+/* Allocation-free variant of the host entry tb_cuda_extract_features_host.
+ * It has no counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc), which cannot create a
+ * tb_cuda_feature_batch.  Host arrays obs [count,4148], mission [count,10],
+ * cameras [count,16384] in; out_features [count,142] out; synchronous, like
+ * the host entry.  The device staging is a static array of the library, for
+ * up to TB_HIP_STATIC_MAX_BATCH environments (8.6 MB, held on every GPU the
+ * library runs on until the process ends), on `stream` (NULL: the null
+ * stream).  Returns 0 with nothing enqueued for NULL pointers, count 0 or
+ * count above TB_HIP_STATIC_MAX_BATCH; 0 also if a copy or the launch
+ * fails.  Every call on a GPU uses that GPU's one array: calls that overlap
+ * on one GPU race. */
+#define TB_HIP_STATIC_MAX_BATCH 256
+int tb_hip_extract_features_host_static(const float *obs, const float *mission,
+                                        const unsigned char *cameras, size_t count,
+                                        float *out_features, void *stream);
+
 /* Per-bin LiDAR transform of the feature kernel, elementwise over `count`
  * floats: -1 for non-finite or negative ranges, otherwise
  * log1p(min(r,120)) / log1pf(120) (reference training.c:65-68).  Exposed so

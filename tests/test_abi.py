@@ -63,6 +63,13 @@ def test_argument_validation_without_gpu():
     assert lib.tb_cuda_extract_features_device(dummy, dummy, None, dummy, 0, None) == 0
     assert lib.tb_cuda_extract_features_device(dummy, dummy, None, dummy, 0x80000000,
                                                None) == 0
+    # Allocation-free host entry: NULL pointers, count 0 and count above its
+    # static staging (TB_HIP_STATIC_MAX_BATCH = 256), before any runtime call.
+    assert lib.tb_hip_extract_features_host_static(None, dummy, dummy, 1, dummy, None) == 0
+    assert lib.tb_hip_extract_features_host_static(dummy, dummy, None, 1, dummy, None) == 0
+    assert lib.tb_hip_extract_features_host_static(dummy, dummy, dummy, 1, None, None) == 0
+    assert lib.tb_hip_extract_features_host_static(dummy, dummy, dummy, 0, dummy, None) == 0
+    assert lib.tb_hip_extract_features_host_static(dummy, dummy, dummy, 257, dummy, None) == 0
     # Strided entry additionally rejects misaligned float rows.
     assert lib.tb_hip_extract_features_strided_device(dummy, 4148 * 4 + 2, dummy, 40, None, 0,
                                                       dummy, 1, None) == 0

@@ -27,6 +27,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "turbinator/training/cuda_features.h"
 #include "turbinator/training/hip_features.h"
 #include "xcd_order.h"
@@ -667,6 +669,76 @@ extern "C" int tb_hip_extract_features_depth_device(const float *obs, const floa
     rows.capacity = 0;
     rows.batch = batch_size;
     return launch_features(rows, reinterpret_cast<hipStream_t>(stream));
+}
+
+// Staging of tb_hip_extract_features_host_static: the inputs and features of
+// up to TB_HIP_STATIC_MAX_BATCH environments, one array per GPU (every GPU
+// the library runs on holds its own copy), sections on 256 bytes.  Host code
+// never passes `scratch` itself to a kernel or copy: its name there stands
+// for the host-side shadow, not a device address.  The device address comes
+// from hipGetSymbolAddress, once per device, with that device current.
+namespace {
+constexpr size_t kStaticMax = TB_HIP_STATIC_MAX_BATCH;
+constexpr size_t align_section(size_t x) { return (x + 255) & ~(size_t)255; }
+constexpr size_t kStaticObs = 0;
+constexpr size_t kStaticMission = align_section(kStaticObs + kStaticMax * kObsDim * sizeof(float));
+constexpr size_t kStaticCameras = align_section(kStaticMission + kStaticMax * 10 * sizeof(float));
+constexpr size_t kStaticFeatures = align_section(kStaticCameras + kStaticMax * 16384);
+constexpr size_t kStaticBytes = align_section(kStaticFeatures + kStaticMax * kFeatureDim * sizeof(float));
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+namespace {
+// scratch's device address per device, 0 until first looked up.
+std::atomic<unsigned char *> scratch_address[kMaxDevices];
+
+unsigned char *static_staging() {
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices)
+        return nullptr;
+    unsigned char *address = scratch_address[device].load(std::memory_order_acquire);
+    if (address) return address;
+    void *found = nullptr;
+    if (hipGetSymbolAddress(&found, HIP_SYMBOL(scratch)) != hipSuccess || !found) return nullptr;
+    address = static_cast<unsigned char *>(found);
+    scratch_address[device].store(address, std::memory_order_release);
+    return address;
+}
+}  // namespace
+
+// tb_cuda_extract_features_host (src/cuda/features.cu:62-88) with the staging
+// above instead of a handle's buffers: the same copies in, the device entry,
+// the copy out and the wait, on the caller's stream.  No allocation: the
+// only runtime calls are hipGetDevice, hipGetSymbolAddress (first call on a
+// device), hipMemcpyAsync, the launch and hipStreamSynchronize.  Nothing in
+// the staging has to start at zero: each call writes the rows it reads.
+extern "C" int tb_hip_extract_features_host_static(const float *obs, const float *mission,
+                                                   const unsigned char *cameras, size_t count,
+                                                   float *out_features, void *stream) {
+    if (!obs || !mission || !cameras || !out_features || count == 0 || count > kStaticMax)
+        return 0;
+    unsigned char *staging = static_staging();
+    if (!staging) return 0;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    float *d_obs = reinterpret_cast<float *>(staging + kStaticObs);
+    float *d_mission = reinterpret_cast<float *>(staging + kStaticMission);
+    unsigned char *d_cameras = staging + kStaticCameras;
+    float *d_features = reinterpret_cast<float *>(staging + kStaticFeatures);
+    if (hipMemcpyAsync(d_obs, obs, count * kObsDim * sizeof(float), hipMemcpyHostToDevice, s) !=
+            hipSuccess ||
+        hipMemcpyAsync(d_mission, mission, count * 10 * sizeof(float), hipMemcpyHostToDevice,
+                       s) != hipSuccess ||
+        hipMemcpyAsync(d_cameras, cameras, count * 16384, hipMemcpyHostToDevice, s) !=
+            hipSuccess)
+        return 0;
+    if (!tb_cuda_extract_features_device(d_obs, d_mission, d_cameras, d_features, count, stream))
+        return 0;
+    if (hipMemcpyAsync(out_features, d_features, count * kFeatureDim * sizeof(float),
+                       hipMemcpyDeviceToHost, s) != hipSuccess)
+        return 0;
+    return hipStreamSynchronize(s) == hipSuccess;
 }
 
 extern "C" int tb_hip_lidar_transform_device(const float *ranges, float *out, size_t count,

@@ -141,6 +141,23 @@ class FeatureBatch:
         self.destroy()
 
 
+STATIC_MAX_BATCH = 256  # TB_HIP_STATIC_MAX_BATCH in hip_features.h
+
+
+def extract_features_host_static(obs: np.ndarray, mission: np.ndarray, cameras: np.ndarray,
+                                 count: int, out: np.ndarray, stream=None) -> int:
+    """tb_hip_extract_features_host_static: the host entry without a handle,
+    staged in the library's static device array (count <= STATIC_MAX_BATCH)."""
+    for a, dt, width in ((obs, np.float32, OBS_DIM), (mission, np.float32, MISSION_DIM),
+                         (cameras, np.uint8, CAMERA_BYTES), (out, np.float32, FEATURE_DIM)):
+        if a.dtype != dt or not a.flags.c_contiguous or a.size < count * width:
+            raise ValueError("host arrays must be C-contiguous with count rows of the "
+                             "reference layout")
+    return hip_lib().tb_hip_extract_features_host_static(
+        obs.ctypes.data, mission.ctypes.data, cameras.ctypes.data, count, out.ctypes.data,
+        _stream(stream))
+
+
 def feature_batch_error(handle) -> str:
     """tb_cuda_feature_batch_error for a raw handle (None -> NULL)."""
     return hip_lib().tb_cuda_feature_batch_error(handle).decode()
@@ -215,4 +232,5 @@ __all__ = ["extract_features_device", "extract_features_strided_device",
            "extract_features_diagnostics_device", "extract_features_indexed_device",
            "extract_features_depth_device", "lidar_transform_device",
            "onboard_tactical_prior_device", "actor_inputs_device", "synchronize", "FeatureBatch",
-           "feature_batch_error", "FeaturePipeline"]
+           "feature_batch_error", "FeaturePipeline", "extract_features_host_static",
+           "STATIC_MAX_BATCH"]

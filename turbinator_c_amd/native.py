@@ -44,6 +44,8 @@ HIP_SIGNATURES = {
         (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "tb_hip_extract_features_depth_device":
         (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "tb_hip_extract_features_host_static":
+        (c_int, [c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "tb_hip_lidar_transform_device": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "tb_hip_actor_inputs_device": (c_int, [c_void_p] * 9 + [c_size_t, c_void_p]),
     "tb_hip_sac_actor_packed_bytes": (c_size_t, [c_int]),
