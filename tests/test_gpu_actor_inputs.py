@@ -155,6 +155,90 @@ def test_config_16384(torch_cuda, hip):
     check_h2(sub, want, "16384")
 
 
+def _call_all(torch, hip, d_in, out, n, stream_arg, s_sync):
+    assert hip.actor_inputs_device(*d_in, *out, n, stream_arg) == 1
+    assert hip.synchronize(s_sync) == 1
+    return [t[:n].cpu().numpy().view(np.uint32).copy() for t in out]
+
+
+def _device_batch(torch, n, seed):
+    b = synth.make_batch(n, seed=seed, threads=16)
+    d_in = [torch.from_numpy(a).cuda() for a in (b.obs, b.mission, b.cameras)]
+    out = [torch.full(shape, float("nan"), dtype=torch.float32, device="cuda")
+           for shape in ((n, 91), (n, 49), (n, 24), (n, 15), (n, 6, 16, 128), (n, 4, 64, 64))]
+    return d_in, out
+
+
+def test_overlap_threshold_and_null_stream(torch_cuda, hip):
+    """From 2,048 environments with plane outputs the scan and control
+    kernels run on a second stream beside the plane kernel.  The 2,048-row
+    call must equal the 2,047-row call (one stream) on their common rows, bit
+    for bit, and a call on the null stream must equal one on a torch stream."""
+    torch = torch_cuda
+    note("actor inputs: overlap threshold 2047 / 2048, null stream")
+    d_in, out = _device_batch(torch, 2048, seed=2048)
+    s = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    two_streams = _call_all(torch, hip, d_in, out, 2048, s, s)
+    for t in out:
+        t.fill_(float("nan"))
+    torch.cuda.synchronize()
+    one_stream = _call_all(torch, hip, d_in, out, 2047, s, s)
+    for name, g, w in zip(("proprio", "mission", "tactical", "prior", "lidar", "luma"),
+                          two_streams, one_stream):
+        assert np.array_equal(g[:2047], w), f"{name}: 2048-row call differs from 2047-row call"
+    for t in out:
+        t.fill_(float("nan"))
+    torch.cuda.synchronize()
+    null = _call_all(torch, hip, d_in, out, 2048, None, None)
+    for name, g, w in zip(("proprio", "mission", "tactical", "prior", "lidar", "luma"),
+                          null, two_streams):
+        assert np.array_equal(g, w), f"{name}: null-stream call differs"
+
+
+def test_concurrent_callers_on_their_own_streams(torch_cuda, hip):
+    """Two host threads, each on its own stream, call the entry at 4,096
+    environments three times each at once: the calls share the device's
+    second stream one fork ... join at a time, and every result must equal
+    the same call made alone."""
+    import threading
+
+    torch = torch_cuda
+    note("actor inputs: two host threads, 4096 envs, own streams")
+    jobs = [_device_batch(torch, 4096, seed=4096 + k) for k in range(2)]
+    s0 = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    alone = [_call_all(torch, hip, d_in, out, 4096, s0, s0) for d_in, out in jobs]
+    for _, out in jobs:
+        for t in out:
+            t.fill_(float("nan"))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in jobs]
+    results, errors = [None, None], []
+
+    def worker(k):
+        try:
+            d_in, out = jobs[k]
+            for _ in range(3):
+                assert hip.actor_inputs_device(*d_in, *out, 4096, streams[k]) == 1
+            assert hip.synchronize(streams[k]) == 1
+            results[k] = [t.cpu().numpy().view(np.uint32).copy() for t in out]
+        except Exception as exc:  # reported below, on the test's thread
+            errors.append(repr(exc))
+
+    threads = [threading.Thread(target=worker, args=(k,)) for k in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads), "a caller thread did not finish"
+    assert not errors, errors
+    for k in range(2):
+        for name, g, w in zip(("proprio", "mission", "tactical", "prior", "lidar", "luma"),
+                              results[k], alone[k]):
+            assert np.array_equal(g, w), f"thread {k}: {name} differs from the call made alone"
+
+
 def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
     """As for the onboard entry: 263,144 rows tiled from 4,096 distinct
     environments (the scan waves form a second group of 64 frames, and the
