@@ -239,6 +239,35 @@ def test_concurrent_callers_on_their_own_streams(torch_cuda, hip):
             assert np.array_equal(g, w), f"thread {k}: {name} differs from the call made alone"
 
 
+def test_graph_capture_with_the_second_stream(torch_cuda, hip):
+    """A call captured into a HIP graph after the device's second stream
+    exists: the fork and join events bring that stream into the capture.
+    Each of three replays, with eager work and a refill of the outputs
+    between them, must equal the eager call bit for bit."""
+    torch = torch_cuda
+    note("actor inputs: graph capture at 4096 envs, 3 replays")
+    d_in, out = _device_batch(torch, 4096, seed=4242)
+    s0 = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    eager = _call_all(torch, hip, d_in, out, 4096, s0, s0)   # also makes the second stream
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cs = torch.cuda.current_stream()
+        assert hip.actor_inputs_device(*d_in, *out, 4096, cs) == 1
+    scratch = torch.zeros(1 << 20, device="cuda")
+    for rep in range(3):
+        for t in out:
+            t.fill_(float("nan"))
+        scratch.add_(1.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [t.cpu().numpy().view(np.uint32).copy() for t in out]
+        for name, g, w in zip(("proprio", "mission", "tactical", "prior", "lidar", "luma"),
+                              got, eager):
+            assert np.array_equal(g, w), f"replay {rep}: {name} differs from the eager call"
+
+
 def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
     """As for the onboard entry: 263,144 rows tiled from 4,096 distinct
     environments (the scan waves form a second group of 64 frames, and the
