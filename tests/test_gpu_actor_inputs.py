@@ -138,7 +138,7 @@ def test_optional_outputs_and_ragged(torch_cuda, hip):
 
 
 def test_config_16384(torch_cuda, hip):
-    """BASELINE's 16,384-environment batch: channels and luma bit-exact for
+    """The benchmark's 16,384-environment batch: channels and luma bit-exact for
     every environment against numpy; the rest against the oracle on 512
     sampled environments."""
     note("actor inputs 16384 envs")
