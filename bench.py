@@ -626,12 +626,23 @@ def main() -> int:
     secondary = None
     if not args.no_secondary:
         # BASELINE.json configurations 3 (literal fp32 depth cameras) and 5
-        # (strided replay records), each with its own roofline fraction.
-        log("[bench] secondary: configuration 3 fp32 depth, configuration 5")
+        # (strided replay records), each with its own roofline fraction; then
+        # the other rows of the path on the headline batch: the onboard
+        # tactical + prior entry, the 618M actor's fused sensor preparation
+        # and the compact actor (alone and behind the feature kernel).
+        log("[bench] secondary: configuration 3 fp32 depth, configuration 5, onboard, "
+            "actor preparation, compact actor")
         secondary = []
         _leg_depth(torch, sets, threads, max(args.steps // 5, 20), secondary)
         torch.cuda.empty_cache()
         _leg_c5(torch, threads, max(args.steps // 2, 40), secondary)
+        torch.cuda.empty_cache()
+        tac = torch.empty((BATCH, 24), dtype=torch.float32, device="cuda")
+        pri = torch.empty((BATCH, 15), dtype=torch.float32, device="cuda")
+        _leg_onboard(torch, sets, max(args.steps, 40), secondary, tac, pri)
+        _leg_actor_prep(torch, sets, max(args.steps // 2, 40), secondary, tac, pri)
+        _leg_sac_actor(torch, sets, max(args.steps, 40), secondary)
+        del tac, pri
         torch.cuda.empty_cache()
     bytes_per_call = BYTES_PER_ENV * BATCH
     achieved = bytes_per_call / per_call / 1e9
