@@ -5,11 +5,11 @@ tb_sac_act_features bit for bit (tests/test_sac_actor_oracle.py).
 The matrix cores sum in another order than the reference's sequential loop,
 each product is formed from two-piece fp16 splits of its operands with the
 lo*lo cross term (at most 2^-22 of the product) left out, each instruction's
-block sum drops the bits of its products that lie more than about 2^-24
-below the block's largest (measured on gfx950: at most 4.4 u sum|p| per
-instruction over 131k random blocks, 0.6 u on average, u = 2^-24, and
-biased toward zero, where the reference's sequential fp32 sum rounds to
-nearest), and tanhf / expf / logf are the device library's.  So each
+block sum drops the bits of its products that lie more than 2^-24 below the
+largest of their group of eight before rounding (tests/csrc/check_mfma_sum.hip:
+at most 3.8 u sum|p| per instruction over 262,144 random outputs, 0.4 u on
+average, u = 2^-24, where the reference's sequential fp32 sum rounds every
+step to nearest), and tanhf / expf / logf are the device library's.  So each
 output is held to a bound set by its own conditioning:
   * raw outputs: eps (1 + S2 + J), eps = 1e-6 (about 17 u), the first-order
     effect of an error of at most eps S_l in every pre-activation of every

@@ -14,15 +14,15 @@
 // normal fp16, |err| <= 2^-22 |x|.  A product is summed as the three cross
 // terms hi·hi, hi·lo and lo·hi: the dropped lo·lo and the two operands'
 // errors come to at most 3·2^-22 |w x| (about 7e-7), and each cross product
-// of two fp16 values is exact.  The instruction's block sum is not rounded
-// to nearest, though: bits of a product more than about 2^-24 below the
-// largest product of its block are dropped (measured on gfx950 over 131k
-// random blocks: at most 4.4 u sum|p| per instruction, 0.6 u on average,
-// u = 2^-24, biased toward zero).  A layer's error is therefore a small
-// multiple of u sum|w x|, the form of the reference's sequential fp32 sum
-// too, and a hidden unit whose summands cancel passes it on to the outputs
-// as the reference's does.  Three fp16 steps
-// take 3/16 of the fp32 matrix-core time of the same product.  (The
+// of two fp16 values is exact.  The instruction's block sum is not the
+// correctly rounded sum, though: the bits of a product that lie more than
+// 2^-24 below the largest product of its group of eight are dropped before
+// the sum is rounded (tests/csrc/check_mfma_sum.hip; over 262,144 random
+// outputs the error is at most 3.8 u sum|p|, 0.4 u on average, u = 2^-24).
+// A layer's error is therefore a small multiple of u sum|w x|, the form of
+// the reference's sequential fp32 sum too, and a hidden unit whose summands
+// cancel passes it on to the outputs as the reference's does.  Three fp16
+// steps take 3/16 of the fp32 matrix-core time of the same product.  (The
 // two-piece fp16 split with three products is the scheme of Ootomo and
 // Yokota, "Recovering single precision accuracy from Tensor Cores while
 // surpassing the FP32 theoretical peak performance", IJHPCA 36(4), 2022;
