@@ -1632,17 +1632,24 @@ SideStream side_streams[kMaxDevices];
 // The current device's side stream (default priority, non-blocking), made
 // on first use.  nullptr when it cannot be made, and while `s` is being
 // captured into a graph before it exists (a capture may use one made
-// earlier: the fork and join events bring it into the capture).
+// earlier: the fork and join events bring it into the capture).  A failed
+// query or creation is cleared from the runtime's last error, so the call
+// goes on with one stream and its own launch check stays meaningful.
 SideStream *side_stream(hipStream_t s) {
     int dev = -1;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
     SideStream &ss = side_streams[dev];
     int state = ss.state.load(std::memory_order_acquire);
     if (state == 0) {
         hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(s, &capture) != hipSuccess ||
-            capture != hipStreamCaptureStatusNone)
+        if (hipStreamIsCapturing(s, &capture) != hipSuccess) {
+            (void)hipGetLastError();
             return nullptr;
+        }
+        if (capture != hipStreamCaptureStatusNone) return nullptr;
         std::lock_guard<std::mutex> made(ss.order);
         state = ss.state.load(std::memory_order_acquire);
         if (state == 0) {
@@ -1651,6 +1658,7 @@ SideStream *side_stream(hipStream_t s) {
                 hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) == hipSuccess &&
                 hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) == hipSuccess;
             state = ok ? 1 : -1;
+            if (!ok) (void)hipGetLastError();
             ss.state.store(state, std::memory_order_release);
         }
     }
