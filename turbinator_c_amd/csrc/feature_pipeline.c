@@ -79,6 +79,16 @@ static int fp_fail(tb_hip_feature_pipeline *p, const char *stage, hipError_t sta
     return 0;
 }
 
+/* A submit that fails after it has queued work waits for that work before it
+ * returns, so the caller may refill the slot's pinned arrays at once. */
+static int fp_fail_queued(tb_hip_feature_pipeline *p, fp_slot *q, const char *stage,
+                          hipError_t status) {
+    fp_fail(p, stage, status);
+    (void)hipStreamSynchronize(q->stream);
+    (void)hipGetLastError();
+    return 0;
+}
+
 static int fp_valid_slot(const tb_hip_feature_pipeline *p, int slot) {
     return p && slot >= 0 && slot < p->nslots;
 }
@@ -107,8 +117,10 @@ tb_hip_feature_pipeline *tb_hip_feature_pipeline_create(int device_id, size_t ma
             tb_hip_feature_pipeline_destroy(p);
             return NULL;
         }
-        if (hipHostGetDevicePointer((void **)&q->mapped, q->host, 0) != hipSuccess)
+        if (hipHostGetDevicePointer((void **)&q->mapped, q->host, 0) != hipSuccess) {
             q->mapped = NULL;  /* direct submits report this */
+            (void)hipGetLastError();
+        }
         if (hipMalloc((void **)&q->device, bytes) != hipSuccess) {
             q->device = NULL;
             tb_hip_feature_pipeline_destroy(p);
@@ -169,11 +181,11 @@ int tb_hip_feature_pipeline_submit(tb_hip_feature_pipeline *p, int slot, size_t 
         if (status != hipSuccess) return fp_fail(p, "copy observations", status);
         status = hipMemcpyAsync(q->device + off_mission(n), q->host + off_mission(n),
                                 count * FP_MISSION_BYTES, hipMemcpyHostToDevice, q->stream);
-        if (status != hipSuccess) return fp_fail(p, "copy mission", status);
+        if (status != hipSuccess) return fp_fail_queued(p, q, "copy mission", status);
         if (with_cameras) {
             status = hipMemcpyAsync(q->device + off_cameras(n), q->host + off_cameras(n),
                                     count * FP_CAMERA_BYTES, hipMemcpyHostToDevice, q->stream);
-            if (status != hipSuccess) return fp_fail(p, "copy cameras", status);
+            if (status != hipSuccess) return fp_fail_queued(p, q, "copy cameras", status);
         }
     }
     if (!tb_cuda_extract_features_device((const float *)q->device,
@@ -181,10 +193,10 @@ int tb_hip_feature_pipeline_submit(tb_hip_feature_pipeline *p, int slot, size_t 
                                          with_cameras ? q->device + off_cameras(n) : NULL,
                                          (float *)(q->device + off_features(n)), count,
                                          q->stream))
-        return fp_fail(p, "extract features", launch_status());
+        return fp_fail_queued(p, q, "extract features", launch_status());
     status = hipMemcpyAsync(q->host + off_features(n), q->device + off_features(n),
                             count * FP_FEATURE_BYTES, hipMemcpyDeviceToHost, q->stream);
-    if (status != hipSuccess) return fp_fail(p, "copy features", status);
+    if (status != hipSuccess) return fp_fail_queued(p, q, "copy features", status);
     q->count = count;
     q->in_flight = 1;
     return 1;
