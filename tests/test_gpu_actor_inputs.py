@@ -170,27 +170,27 @@ def _device_batch(torch, n, seed):
 
 
 def test_overlap_threshold_and_null_stream(torch_cuda, hip):
-    """From 2,048 environments with plane outputs the scan and control
-    kernels run on a second stream beside the plane kernel.  The 2,048-row
-    call must equal the 2,047-row call (one stream) on their common rows, bit
+    """From 1,536 environments with plane outputs the scan and control
+    kernels run on a second stream beside the plane kernel.  The 1,536-row
+    call must equal the 1,535-row call (one stream) on their common rows, bit
     for bit, and a call on the null stream must equal one on a torch stream."""
     torch = torch_cuda
-    note("actor inputs: overlap threshold 2047 / 2048, null stream")
-    d_in, out = _device_batch(torch, 2048, seed=2048)
+    note("actor inputs: overlap threshold 1535 / 1536, null stream")
+    d_in, out = _device_batch(torch, 1536, seed=1536)
     s = torch.cuda.current_stream()
     torch.cuda.synchronize()
-    two_streams = _call_all(torch, hip, d_in, out, 2048, s, s)
+    two_streams = _call_all(torch, hip, d_in, out, 1536, s, s)
     for t in out:
         t.fill_(float("nan"))
     torch.cuda.synchronize()
-    one_stream = _call_all(torch, hip, d_in, out, 2047, s, s)
+    one_stream = _call_all(torch, hip, d_in, out, 1535, s, s)
     for name, g, w in zip(("proprio", "mission", "tactical", "prior", "lidar", "luma"),
                           two_streams, one_stream):
-        assert np.array_equal(g[:2047], w), f"{name}: 2048-row call differs from 2047-row call"
+        assert np.array_equal(g[:1535], w), f"{name}: 1536-row call differs from 1535-row call"
     for t in out:
         t.fill_(float("nan"))
     torch.cuda.synchronize()
-    null = _call_all(torch, hip, d_in, out, 2048, None, None)
+    null = _call_all(torch, hip, d_in, out, 1536, None, None)
     for name, g, w in zip(("proprio", "mission", "tactical", "prior", "lidar", "luma"),
                           null, two_streams):
         assert np.array_equal(g, w), f"{name}: null-stream call differs"

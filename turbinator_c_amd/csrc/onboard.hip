@@ -1614,11 +1614,12 @@ __global__ __launch_bounds__(kStreamThreads) void actor_stream_kernel(ActorRows 
 // and control workgroups fit beside it, and their latency-bound chains
 // overlap its streams.  Measured on the entry (identical outputs): 77.8 ->
 // 68.3 us at 2,048 environments, 128.7 -> 118.4 at 4,096, 230.2 -> 222.6 at
-// 8,192 and 433.4 -> 428.6 at 16,384; the fork and join cost about 19 us at
-// 32 environments and 6.5 us at 1,024, so smaller batches keep one stream.  The scan alone on the second stream,
+// 8,192 and 433.4 -> 428.6 at 16,384, 61.7 -> 59.4 at 1,536; the fork and
+// join cost about 19 us at 32 environments, 6.5 us at 1,024 and 2.7 us at
+// 1,280, so smaller batches keep one stream.  The scan alone on the second stream,
 // with the controller after the join, measured 437.9 us: it is the
 // controller that gains from running beside the planes.
-constexpr size_t kOverlapMinBatch = 2048;
+constexpr size_t kOverlapMinBatch = 1536;
 constexpr int kMaxDevices = 64;
 
 struct SideStream {
