@@ -8,13 +8,17 @@ reference's own src/training/training.c).
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import c_float, c_int, c_size_t, c_void_p
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_ORACLE = HERE / "liboracle.so"
+# TB_ORACLE_LIB names another build of the restatement: the mutation test
+# (tests/test_onboard_oracle_mutants.py) runs the pin tests against copies with
+# a planted mistake.
+LIB_ORACLE = Path(os.environ.get("TB_ORACLE_LIB") or HERE / "liboracle.so")
 LIB_REF = HERE / "_ref" / "libref_training.so"
 
 OBS, MISSION, CAMERA, FEATURES, DIAG_BYTES = 4148, 10, 16384, 142, 432
@@ -29,7 +33,7 @@ def lib() -> ctypes.CDLL:
     global _orc
     if _orc is None:
         if not LIB_ORACLE.exists():
-            raise RuntimeError("oracle/liboracle.so not built (make -C oracle)")
+            raise RuntimeError(f"{LIB_ORACLE} not built (make -C oracle)")
         l = ctypes.CDLL(str(LIB_ORACLE))
         l.orc_features_env.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p]
         l.orc_features_env.restype = None

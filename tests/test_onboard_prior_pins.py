@@ -38,11 +38,10 @@ wrong condition) fails at least one of them:
   rotation matrices (heading and body frames as matrix products) on random
   attitudes, arms, goals and cannon states.
 
-Planting each of 56 single mistakes in a copy of the oracle (swapped or
-altered constants, flipped signs, transposed rows or arms, moved thresholds)
-makes this file or the reference goldens fail for 55 of them; the one left
-changes the 0.9 pi/4 inner-gimbal clamp, which no input reaches (the inner
-command is at most asin(0.44) < 0.9 pi/4).
+tests/test_onboard_oracle_mutants.py plants single mistakes in copies of the
+oracle (swapped or altered constants, flipped signs, transposed rows or arms,
+moved thresholds) and requires this file or the reference goldens to fail
+for every one that an input can reach.
 
 Expected values are evaluated in float64 from the float32 inputs; the oracle
 runs in float32, so the comparisons carry a 2e-5 bar (the kernel's own bar
@@ -371,6 +370,52 @@ def test_heavy_cargo(px, pz, vx, des_vz, des_ax):
                 dict(px=px, pz=pz, vx=vx, payload=1.0), {2: 1.0}, HEAVY, mass=HEAVY_MASS)
 
 
+# The heavy-cargo limits below are hidden at the states above by a clamp
+# further down the law: 52 N of force is only 0.71 m/s^2 at 73 kg, so every
+# horizontal acceleration above that is clipped, and a steep vertical command
+# meets the -1.8 floor.  Each state here makes the named limit the binding one
+# and keeps everything after it unclipped (asserted at the spool used).
+
+def check_heavy_binding(des_ax, des_vz, obs_kw):
+    """check_level for heavy cargo, with the force and the vertical
+    acceleration asserted inside their caps at the spool the check uses."""
+    vx, vz = obs_kw.get("vx", 0.0), obs_kw.get("vz", 0.0)
+    assert abs(HEAVY_MASS * des_ax + 0.4 * vx) < 52.0
+    raw_az = lambda s: 5.0 * (des_vz - vz) - az_actual(s, HEAVY_MASS)
+    law = lambda s, m: (des_ax, 0.0, clamp(raw_az(s), -1.8, 5.5))
+    s = pick_spool(lambda sp: level_mixer(sp, HEAVY_MASS, *law(sp, HEAVY_MASS), vx=vx,
+                                          **HEAVY))
+    assert -1.8 < raw_az(s) < 5.5
+    check_level(law, dict(obs_kw, payload=1.0), {2: 1.0}, HEAVY, mass=HEAVY_MASS, s=s)
+
+
+def test_heavy_cargo_transit_speed_cap():
+    # 10 m from the pad: des_vx = clamp(0.75 * 10, +-2.65) = 2.65 (:257); at
+    # vx = 2.45 that asks 2.4 * 0.2 m/s^2, 36 N; transit height 1.2 + 0.28 * 10
+    check_heavy_binding(2.4 * (2.65 - 2.45), 1.3 * (1.2 + 0.28 * 10.0 - 3.5),
+                        dict(px=5.0, pz=3.5, vx=2.45))
+
+
+def test_heavy_cargo_climb_clamp():
+    # 0.4 m up, 0.1 m short of the pad, no landing flag (so no land-idle):
+    # cargo descent law clamp(1.6 (0.64 - 0.4), -0.3, 0.18) = 0.18 (:264)
+    assert 1.6 * (0.64 - 0.4) > 0.18
+    check_heavy_binding(2.4 * 0.75 * 0.1, 0.18, dict(px=14.9, pz=0.4))
+
+
+def test_heavy_cargo_transit_sink_cap():
+    # 3 m out, 1.46 m above the 2.04 m transit height: 1.3 * -1.46 -> -1.05
+    # (:270); sinking at 1 m/s already, so the command stays above -1.8
+    assert 1.3 * (1.2 + 0.28 * 3.0 - 3.5) < -1.05
+    check_heavy_binding(2.4 * (0.75 * 3.0 - 2.0), -1.05, dict(px=12.0, pz=3.5, vx=2.0, vz=-1.0))
+
+
+def test_heavy_cargo_acceleration_cap():
+    # 2.4 (2.25 + 280) -> 2.2 (:276); the 0.4 vx damping (-112 N) brings
+    # 73 * 2.2 = 160.6 N under the 52 N force cap, which a 2.6 cap would not
+    check_heavy_binding(2.2, 1.3 * (1.2 + 0.28 * 3.0 - 2.0), dict(px=12.0, pz=2.0, vx=-280.0))
+
+
 def test_light_cargo_uses_standard_law():
     # no payload: standard law towards (15, 0, pz)
     check_level(lambda s, m: (2.4 * 0.9, 0.0, -0.8 * az_actual(s, m)),
@@ -390,11 +435,15 @@ def rel(v, lim=0.9995):
 
 
 @pytest.mark.parametrize("m7,m8,vx,vy", [(0.05, 0.02, 0.5, 0.1), (0.1, 0.1, 0.8, 1.0),
-                                         (0.1, 0.02, 1.5, 0.1), (0.02, 0.1, 0.2, 1.5)])
+                                         (0.1, 0.02, 1.5, 0.1), (0.02, 0.1, 0.2, 1.5),
+                                         (math.tanh(0.15), math.tanh(0.07), 1.0, 1.0),
+                                         (math.tanh(0.15), math.tanh(0.0665), 1.0, 1.0)])
 def test_lateral(m7, m8, vx, vy):
     # m[4] > 0.75, m[5] > 0.25: goal = position + 20 atanh(m[7..8]); gains
-    # 0.95 / 1.05; y cap 3.4, x cap 1.45 when |up_y| > 1.35 else 3.8; force
-    # cap 125 N, inner limit 0.44
+    # 0.95 / 1.05; y cap 3.4, x cap 1.45 when |up_y| > 1.35 else 3.8 (:287);
+    # force cap 125 N, inner limit 0.44.  The last two states put |up_y| at
+    # 1.40 and 1.33, either side of the threshold, with 0.95 up_x = 2.85 above
+    # the 1.45 cap
     ux, uy = rel(m7), rel(m8)
     cap_x = 1.45 if abs(uy) > 1.35 else 3.8
     dvx = clamp(0.95 * ux, -cap_x, cap_x)
@@ -435,6 +484,39 @@ def test_headroom_excess(ox, s):
     assert 0.9 * abs(ox) > 3.95 - 2.55
     check_level(law, dict(pz=12.0, ox=ox), INV, dict(headroom=True), s=s,
                 expect_unsaturated=False)
+
+
+@pytest.mark.parametrize("tilt,px,mission", [
+    (0.60, 1.0, {}),            # standard law: headroom from cos(tilt) = 0.825 < 0.88
+    (0.60, -2.0, {}),
+    (0.30, 1.0, INV),           # inversion mission: headroom at any tilt
+    (0.17, -1.5, INV),
+    (0.10, 1.0, INV)])          # below 0.15 rad: no reduction
+def test_headroom_tilt_scales_horizontal_force(tilt, px, mission):
+    """Pitched hover with headroom (:318-324): the world horizontal force is
+    scaled by clamp(1 - 1.5 max(tilt - 0.15, 0), 0, 1).  At a pure pitch the
+    yaw is 0, so the body force equals the world force, and with the outer
+    gimbals at zero the inner gimbals carry it alone: arm 0 takes
+    asin(0.5 fx / thrust), arm 2 the negative, arms 1 and 3 nothing
+    (:380-384).  Outer gimbals, cannon and fire flag are at rest."""
+    s = 0.5
+    o = level_obs(s, px=px, pz=14.0 if mission else 8.0)
+    o[6], o[8] = math.cos(tilt / 2.0), math.sin(tilt / 2.0)
+    mis = np.zeros(10, np.float32)
+    for k, v in mission.items():
+        mis[k] = v
+    got = run_prior(o, mis)
+    kp, cap = (0.85, 4.2) if mission else (0.90, 3.0)
+    des_ax = clamp(2.4 * clamp(kp * -px, -cap, cap), -3.8, 3.8)
+    scale = clamp(1.0 - 1.5 * max(tilt - 0.15, 0.0), 0.0, 1.0)
+    fx = clamp(BASE * des_ax * scale, -80.0, 80.0)
+    sin_in = 0.5 * fx / thrust(s)
+    assert abs(sin_in) < 0.32                    # the inner limit does not clip
+    want = np.zeros(15)
+    want[8], want[10] = math.asin(sin_in) / (PI / 4), -math.asin(sin_in) / (PI / 4)
+    want[14] = -0.8
+    err = np.abs(got - want)[4:]
+    assert err.max() <= TOL, f"got {got[4:]}\nwant {want[4:]}"
 
 
 # ---------------------------------------------------------------- arena
@@ -643,30 +725,40 @@ def test_inversion_threshold_is_ct_020():
 
 
 # ---------------------------------------------------------------- BWB
-def bwb_obs(vx, pz=60.0, ox=0.0, oy=0.0, oz=0.0, o44=0.0, o45=0.0, ammo=0.0):
+def bwb_obs(vx, pz=60.0, ox=0.0, oy=0.0, oz=0.0, o44=0.0, o45=0.0, ammo=0.0, bank=0.0):
     o = level_obs(0.5, pz=pz, vx=vx, ox=ox, oy=oy, oz=oz, ammo=ammo)
     o[44], o[45] = o44, o45
+    if bank:
+        o[6], o[7] = math.cos(bank / 2.0), math.sin(bank / 2.0)
     return o
 
 
-def bwb_expect(vx, m, ox=0.0, oy=0.0, oz=0.0, arena=False, speed=22.4, base=0.44):
-    """:432-503 at identity attitude, position (0, 0), speed vx along x."""
+def bwb_expect(vx, m, ox=0.0, oy=0.0, oz=0.0, arena=False, speed=22.4, base=0.44, bank=0.0):
+    """:432-503 at position (0, 0), speed vx along x, attitude level or
+    rolled right by `bank` radians about the body x axis (pitch and yaw 0,
+    so the body speed is vx and the sideslip 0)."""
     brx, bry, brz = (rel(m.get(k, 0.0), 0.9999) for k in (7, 8, 9))
     gx, gy, gz = brx, bry, brz
     course_err = math.atan2(gy, gx)          # ground track along x: course yaw 0
     u_coll = clamp(base + 0.065 * (speed - vx) + 0.018 * gz, 0.12, 0.90)
-    diff_u = clamp(0.90 * clamp(-1.35 * course_err, -0.55, 0.55) - 0.34 * ox, -0.45, 0.45)
+    diff_u = clamp(0.90 * (clamp(-1.35 * course_err, -0.55, 0.55) - bank) - 0.34 * ox,
+                   -0.45, 0.45)
     u0, u1 = clamp(u_coll + diff_u, 0.05, 1.0), clamp(u_coll - diff_u, 0.05, 1.0)
     climb = clamp(0.42 * gz, -5.0, 5.0)
     gamma = math.atan2(climb, max(vx, 14.0))
-    pitch = clamp(0.062831853 + 0.75 * gamma + 0.035 * climb, -0.15, 0.25)
+    cb, sb = math.cos(bank), math.sin(bank)
+    pitch = clamp(0.062831853 + 0.75 * gamma + 0.035 * climb + 0.09 * (1.0 - max(cb, 0.5)),
+                  -0.15, 0.25)
     if vx < 15.5:
         pitch = min(pitch, 0.02)
     theta_dot = 2.20 * pitch
-    psi_dot = 0.35 * course_err
+    # coordinated-turn yaw rate g / max(speed, 12) * tan(-bank), bank within 0.75
+    psi_dot = G / max(vx, 12.0) * math.tan(clamp(-bank, -0.75, 0.75)) + 0.35 * course_err
+    q_up = cb * theta_dot - sb * psi_dot
+    r_left = sb * theta_dot + cb * psi_dot
     gimbal = PI / 6
-    i0 = clamp(0.85 * (theta_dot + oy) + 0.03, -gimbal, gimbal)
-    i1 = clamp(-0.65 * (psi_dot - oz), -gimbal, gimbal)
+    i0 = clamp(0.85 * (q_up + oy) + 0.03, -gimbal, gimbal)
+    i1 = clamp(-0.65 * (r_left - oz), -gimbal, gimbal)
     n = np.zeros(15)
     n[0] = n[2] = 2 * u0 - 1
     n[1] = n[3] = 2 * u1 - 1
@@ -689,6 +781,23 @@ def test_bwb_cruise(vx, m, ox, oy, oz, kw):
         mis[k] = v
     got = run_prior(bwb_obs(vx, ox=ox, oy=oy, oz=oz), mis)
     want = bwb_expect(vx, m, ox, oy, oz, **kw)
+    assert np.abs(got - want).max() <= TOL, f"got {got}\nwant {want}"
+
+
+@pytest.mark.parametrize("vx,bank", [(8.0, 0.3), (8.0, -0.5), (11.0, 0.9), (20.0, 0.3),
+                                     (20.0, -0.2)])
+def test_bwb_banked_turn_rate(vx, bank):
+    """Banked BWB cruise, goal straight ahead (:455-478): the roll enters the
+    differential throttle (0.9 (0 - roll)) and the pitch target; the yaw rate
+    is the coordinated turn g / max(body speed, 12) tan(-roll), roll clamped
+    to 0.75, split into the two gimbal rates by the bank.  Below 12 m/s the
+    12 m/s floor sets it, above it the body speed does."""
+    m = {4: 1.0, 2: 0.5, 7: 0.2}
+    mis = np.zeros(10, np.float32)
+    for k, v in m.items():
+        mis[k] = v
+    got = run_prior(bwb_obs(vx, bank=bank), mis)
+    want = bwb_expect(vx, m, bank=bank)
     assert np.abs(got - want).max() <= TOL, f"got {got}\nwant {want}"
 
 
