@@ -288,8 +288,15 @@ def _leg_onboard(torch, sets, steps, out, tac, pri):
     def onboard_call(i, s):
         o, m, _, _ = sets[i % len(sets)]
         assert features.onboard_tactical_prior_device(o, m, tac, pri, None, BATCH, s) == 1
+    # H2 reads obs[0..47], the 1,536 scan rays (2 heads x 6 elevations x 128
+    # azimuths) and the mission row, and writes 24 + 15 floats.
+    onboard_bytes = 4 * (48 + 1536 + 10 + 24 + 15)
     out.append(_report("onboard tactical+prior (16,384 envs)",
-                       _events_time(torch, onboard_call, steps, SUITE_WARMUP), BATCH, None))
+                       _events_time(torch, onboard_call, steps, SUITE_WARMUP), BATCH,
+                       onboard_bytes,
+                       note="bytes_per_env: proprio, scan rays and mission read once, "
+                            "tactical and prior written once; latency- and issue-bound, "
+                            "not HBM-bound"))
 
 
 def _leg_actor_prep(torch, sets, steps, out, tac, pri):

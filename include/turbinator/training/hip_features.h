@@ -16,6 +16,15 @@
 extern "C" {
 #endif
 
+/* Layout version of these extensions, for callers that size the optional
+ * diagnostics outputs themselves.  The entries kept their names and
+ * signatures across these changes:
+ *   2  TB_HIP_ONBOARD_DIAG_DIM 4 -> 5 (cluster y sum appended to the onboard
+ *      scan diagnostics); diagnostics rows 896 bytes (224 words) -> 432
+ *      bytes (TB_HIP_DIAG_BYTES, layout below)
+ *   3  the diagnostics pointer must be 16-byte aligned (was 4-byte) */
+#define TB_HIP_FEATURES_ABI_VERSION 3
+
 enum {
     TB_HIP_OBS_DIM = 4148,
     TB_HIP_MISSION_DIM = 10,
@@ -77,7 +86,8 @@ int tb_hip_extract_features_indexed_device(const void *obs, size_t obs_stride,
  *                   when cameras is NULL)
  * Sector s = head*32 + el_sector*8 + az_sector and quadrant
  * q = cam*4 + qy*2 + qx, the feature vector's orders.  Same argument rules as
- * tb_cuda_extract_features_device; diagnostics must be 4-byte aligned. */
+ * tb_cuda_extract_features_device; diagnostics must be 16-byte aligned
+ * (returns 0 otherwise): the rows are written with 16-byte stores. */
 int tb_hip_extract_features_diagnostics_device(const float *obs, const float *mission,
                                                const unsigned char *cameras,
                                                float *features, void *diagnostics,
@@ -97,17 +107,20 @@ int tb_hip_extract_features_depth_device(const float *obs, const float *mission,
 
 /* Allocation-free variant of the host entry tb_cuda_extract_features_host.
  * It has no counterpart in the reference: it is for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc), which cannot create a
- * tb_cuda_feature_batch.  Host arrays obs [count,4148], mission [count,10],
- * cameras [count,16384] in; out_features [count,142] out; synchronous, like
- * the host entry.  The device staging is a static array of the library, for
- * up to TB_HIP_STATIC_MAX_BATCH environments (8.6 MB, held on every GPU the
+ * allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc), which cannot create a tb_cuda_feature_batch.  Host arrays obs
+ * [count,4148], mission [count,10], cameras [count,16384] in; out_features
+ * [count,142] out.  Synchronous, like the host entry, and it copies pageable
+ * host memory, so it cannot be captured into a HIP graph: on a stream under
+ * capture it returns 0 with nothing enqueued and the capture intact.  The
+ * device staging is a static array of the library, for up to
+ * TB_HIP_STATIC_MAX_BATCH environments (8.6 MB, held on every GPU the
  * library runs on until the process ends), on `stream` (NULL: the null
  * stream).  Returns 0 with nothing enqueued for NULL pointers, count 0 or
  * count above TB_HIP_STATIC_MAX_BATCH; 0 also if a copy or the launch
- * fails.  Every call on a GPU uses that GPU's one array: calls that overlap
- * on one GPU race. */
+ * fails, after waiting for whatever it had queued, so the host arrays are
+ * free again when it returns.  Every call on a GPU uses that GPU's one
+ * array: calls that overlap on one GPU race. */
 #define TB_HIP_STATIC_MAX_BATCH 256
 int tb_hip_extract_features_host_static(const float *obs, const float *mission,
                                         const unsigned char *cameras, size_t count,

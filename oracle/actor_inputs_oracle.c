@@ -57,10 +57,13 @@ void orc_actor_inputs_env(const float *obs, const float *mission, const uint8_t 
                           : (c < 4 ? (valid ? clamped / 30.0f : 1.0f) : (float)valid);
             }
     }
-    /* network_gpu.cu:482 as C evaluates it: the product and the difference
-     * are rounded separately (a fused multiply-add differs for 158 of the
-     * 256 byte values). */
+    /* network_gpu.cu:482, `(float)b * (1.0f / 255.0f) - 0.5f`, exists only
+     * as CUDA device code, and nvcc's default --fmad=true (the reference's
+     * CMakeLists.txt:32-36 sets no CUDA flags) contracts a product followed
+     * by a difference into one fused multiply-add: one rounding.  Two
+     * roundings, as ISO C evaluates the line, differ for 158 of the 256
+     * byte values. */
     if (luma && cameras)
         for (int p = 0; p < 16384; ++p)
-            luma[p] = (float)cameras[p] * (1.0f / 255.0f) - 0.5f;
+            luma[p] = fmaf((float)cameras[p], 1.0f / 255.0f, -0.5f);
 }

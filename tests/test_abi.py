@@ -70,6 +70,10 @@ def test_argument_validation_without_gpu():
     assert lib.tb_hip_extract_features_host_static(dummy, dummy, dummy, 1, None, None) == 0
     assert lib.tb_hip_extract_features_host_static(dummy, dummy, dummy, 0, dummy, None) == 0
     assert lib.tb_hip_extract_features_host_static(dummy, dummy, dummy, 257, dummy, None) == 0
+    # Diagnostics rows are written with 16-byte stores: a pointer that is
+    # only 4-byte aligned is refused.
+    assert lib.tb_hip_extract_features_diagnostics_device(dummy, dummy, None, dummy,
+                                                          ctypes.c_void_p(20), 1, None) == 0
     # Strided entry additionally rejects misaligned float rows.
     assert lib.tb_hip_extract_features_strided_device(dummy, 4148 * 4 + 2, dummy, 40, None, 0,
                                                       dummy, 1, None) == 0

@@ -5,9 +5,10 @@ Each output is checked against a formulation computed another way:
   * LiDAR channels against numpy float32 array arithmetic on a
     (head, row, az) reshape.  A channel taking head c // 2 instead of c % 2,
     a wrong clamp or a wrong sentinel value fails;
-  * luma against b * fl(1/255) rounded to float, minus 0.5 rounded again,
-    formed in double precision (the product of a byte and a float is exact
-    in double).  A fused multiply-add fails for 158 of the 256 bytes;
+  * luma against b * fl(1/255) - 0.5 formed exactly in double precision and
+    rounded once to float: the fused multiply-add nvcc makes of
+    network_gpu.cu:482 by default.  Two roundings (product, then difference)
+    fail for 158 of the 256 bytes;
   * the 52 symlog scalars against float64 log1p, within 2 ulp, including the
     scale table of network_gpu.cu:287-293, probed one input at a time;
   * mission / tactical / prior placement against orc_onboard_env, whose own
@@ -51,11 +52,11 @@ def numpy_lidar_channels(obs: np.ndarray) -> np.ndarray:
 
 def exact_luma(cameras: np.ndarray) -> np.ndarray:
     c = np.float64(np.float32(1.0) / np.float32(255.0))
-    # b * c is exact in double (8 x 24 significant bits); the first cast is
-    # the product's rounding, and the difference of two floats near 0.5 is
-    # exact in double, so the second cast is the subtraction's rounding.
-    prod = (cameras.astype(np.float64) * c).astype(np.float32).astype(np.float64)
-    return (prod - 0.5).astype(np.float32).reshape(cameras.shape[0], 4, 64, 64)
+    # b * c is exact in double (8 x 24 significant bits, a multiple of 2^-31
+    # below 2), and so is b * c - 0.5: the one cast is the fused
+    # multiply-add's single rounding.
+    return (cameras.astype(np.float64) * c - 0.5).astype(np.float32).reshape(
+        cameras.shape[0], 4, 64, 64)
 
 
 def ulp_distance(a: np.ndarray, b: np.ndarray) -> np.ndarray:
@@ -85,18 +86,20 @@ def test_lidar_and_luma_closed_forms(variant):
 
 
 def test_luma_rounding_matters():
-    """A fused multiply-add differs from the two-rounding evaluation for 158
-    bytes, so the closed form above decides between them."""
+    """The two-rounding evaluation (product rounded, then the difference)
+    differs from the fused multiply-add for 158 bytes, so the closed form
+    above decides between them."""
     b = np.arange(256, dtype=np.float64)
-    fused = (b * np.float64(np.float32(1) / np.float32(255)) - 0.5).astype(np.float32)
+    c = np.float64(np.float32(1) / np.float32(255))
+    two = ((b * c).astype(np.float32).astype(np.float64) - 0.5).astype(np.float32)
     cams = np.tile(np.arange(256, dtype=np.uint8), 64)[None, :]
     obs = np.zeros((1, 4148), np.float32)
     got = oracle.actor_inputs(obs, np.zeros((1, 10), np.float32), cams)["luma"].ravel()[:256]
-    assert int((got != fused).sum()) == 158
-    # 255 * fl(1/255) is just above 1: its rounding gives exactly 1, the
-    # fused form keeps the excess.
-    assert got[0] == -0.5 and got[255] == 0.5
-    assert fused[255] == np.nextafter(np.float32(0.5), np.float32(1))
+    assert int((got != two).sum()) == 158
+    # 255 * fl(1/255) is just above 1: the fused form keeps the excess, the
+    # product's own rounding gives exactly 1.
+    assert got[0] == -0.5 and got[255] == np.nextafter(np.float32(0.5), np.float32(1))
+    assert two[255] == 0.5
 
 
 @pytest.mark.parametrize("variant", [0, 4, 5])

@@ -293,6 +293,39 @@ def test_depth_cameras_config2(torch_cuda, hip):
     assert_feature_parity(got, want, "depth")
 
 
+def test_config4_edge_quarters_depth(torch_cuda, hip):
+    """Configuration 4 with its cameras as BASELINE states them, fp32 depth:
+    quarter 2 holds 37.5 m in every pixel, which quantises to luma 207
+    (255 (1 - 37.5 / 200) = 207.19), so its quadrant means are 207/255
+    exactly (training.c:128-141).  The depth entry must also equal the u8
+    entry on the generator's own luma bytes, bit for bit."""
+    note("config 4: 4096 envs edge quarters, fp32 depth cameras")
+    b = synth.make_batch(4096, seed=42, variant=synth.EDGE_QUARTERS, with_depth=True,
+                         threads=16)
+    assert np.all(b.depth[1024:2048] == np.float32(37.5))
+    luma = oracle.depth_to_luma(b.depth)
+    assert np.all(luma[1024:2048] == 207)
+    got = run_depth(torch_cuda, hip, b.obs, b.mission, b.depth)
+    stats = assert_feature_parity(got, oracle.features(b.obs, b.mission, luma), "c4-depth")
+    assert np.all(got[:1024, 62:126] == -1.0)                       # Q1 all no-return
+    assert np.all(got[1024:2048, 126:142] == np.float32(207) / np.float32(255))  # Q2
+    u8 = run_device(torch_cuda, hip, b.obs, b.mission, b.cameras)
+    assert np.array_equal(got.view(np.uint32), u8.view(np.uint32))
+    note(f"c4 depth stats {stats}")
+
+
+def test_config3_depth_full_16384(torch_cuda, hip):
+    """Configuration 3 as BASELINE states it (16,384 environments of
+    4 x 64 x 64 fp32 depth cameras, 1.07 GB of depth), every environment
+    against the oracle on the quantised bytes."""
+    note("config 3: 16384 envs, fp32 depth cameras, full parity")
+    b = synth.make_batch(16384, seed=42, with_depth=True, threads=16)
+    got = run_depth(torch_cuda, hip, b.obs, b.mission, b.depth)
+    want = oracle.features(b.obs, b.mission, oracle.depth_to_luma(b.depth), threads=16)
+    stats = assert_feature_parity(got, want, "c3-depth")
+    note(f"c3 depth stats {stats}")
+
+
 def test_depth_cameras_special_values(torch_cuda, hip):
     note("fp32 depth cameras, special depth values")
     b = synth.make_batch(64, seed=8, with_depth=True)

@@ -45,3 +45,33 @@ def test_static_host_entry_rejects_more_than_its_staging(hip):
     out = np.full((count, 142), np.nan, np.float32)
     assert hip.extract_features_host_static(b.obs, b.mission, b.cameras, count, out) == 0
     assert np.isnan(out).all()
+
+
+def test_static_host_entry_refuses_a_capturing_stream(torch_cuda, hip):
+    """The entry is synchronous and copies pageable memory, which a stream
+    under graph capture cannot take: it returns 0 with nothing enqueued, the
+    capture ends normally and its graph replays, and afterwards the same
+    stream serves the entry again."""
+    import oracle
+    from tests.conftest import assert_feature_parity
+
+    torch = torch_cuda
+    count = 8
+    note("static host entry on a capturing stream")
+    b = synth.make_batch(count, seed=74)
+    out = np.full((count, 142), np.nan, np.float32)
+    side = torch.cuda.Stream()
+    probe = torch.zeros(64, device="cuda")
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        rc = hip.extract_features_host_static(b.obs, b.mission, b.cameras, count, out,
+                                              torch.cuda.current_stream())
+        probe.add_(1.0)
+    assert rc == 0
+    assert np.isnan(out).all()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert float(probe[0]) == 1.0
+    assert hip.extract_features_host_static(b.obs, b.mission, b.cameras, count, out, side) == 1
+    assert_feature_parity(out, oracle.features(b.obs, b.mission, b.cameras), "after capture")

@@ -581,8 +581,8 @@ extern "C" int tb_hip_extract_features_diagnostics_device(const float *obs, cons
                                                           float *features, void *diagnostics,
                                                           size_t batch_size, void *stream) {
     if (!obs || !mission || !features || !diagnostics || batch_size == 0 ||
-        batch_size > kMaxBatch || (reinterpret_cast<uintptr_t>(diagnostics) & 3u) != 0)
-        return 0;
+        batch_size > kMaxBatch || (reinterpret_cast<uintptr_t>(diagnostics) & 15u) != 0)
+        return 0;  // the rows are written with 16-byte stores
     Rows rows;
     rows.obs = reinterpret_cast<const unsigned char *>(obs);
     rows.obs_stride = kObsDim * sizeof(float);
@@ -712,33 +712,47 @@ unsigned char *static_staging() {
 // above instead of a handle's buffers: the same copies in, the device entry,
 // the copy out and the wait, on the caller's stream.  No allocation: the
 // only runtime calls are hipGetDevice, hipGetSymbolAddress (first call on a
-// device), hipMemcpyAsync, the launch and hipStreamSynchronize.  Nothing in
-// the staging has to start at zero: each call writes the rows it reads.
+// device), hipStreamIsCapturing, hipMemcpyAsync, the launch and
+// hipStreamSynchronize.  Nothing in the staging has to start at zero: each
+// call writes the rows it reads.
+//
+// The call is synchronous and copies pageable host memory, neither of which
+// a stream under graph capture accepts (a refused call would also end the
+// caller's capture), so a capturing stream gets 0 with nothing enqueued.  A
+// failure after the first copy was queued waits for the queued work before
+// returning 0, so the caller may reuse its host arrays at once.
 extern "C" int tb_hip_extract_features_host_static(const float *obs, const float *mission,
                                                    const unsigned char *cameras, size_t count,
                                                    float *out_features, void *stream) {
     if (!obs || !mission || !cameras || !out_features || count == 0 || count > kStaticMax)
         return 0;
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &capture) != hipSuccess ||
+        capture != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return 0;
+    }
     unsigned char *staging = static_staging();
     if (!staging) return 0;
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     float *d_obs = reinterpret_cast<float *>(staging + kStaticObs);
     float *d_mission = reinterpret_cast<float *>(staging + kStaticMission);
     unsigned char *d_cameras = staging + kStaticCameras;
     float *d_features = reinterpret_cast<float *>(staging + kStaticFeatures);
-    if (hipMemcpyAsync(d_obs, obs, count * kObsDim * sizeof(float), hipMemcpyHostToDevice, s) !=
-            hipSuccess ||
+    const bool ok =
+        hipMemcpyAsync(d_obs, obs, count * kObsDim * sizeof(float), hipMemcpyHostToDevice, s) ==
+            hipSuccess &&
         hipMemcpyAsync(d_mission, mission, count * 10 * sizeof(float), hipMemcpyHostToDevice,
-                       s) != hipSuccess ||
-        hipMemcpyAsync(d_cameras, cameras, count * 16384, hipMemcpyHostToDevice, s) !=
-            hipSuccess)
-        return 0;
-    if (!tb_cuda_extract_features_device(d_obs, d_mission, d_cameras, d_features, count, stream))
-        return 0;
-    if (hipMemcpyAsync(out_features, d_features, count * kFeatureDim * sizeof(float),
-                       hipMemcpyDeviceToHost, s) != hipSuccess)
-        return 0;
-    return hipStreamSynchronize(s) == hipSuccess;
+                       s) == hipSuccess &&
+        hipMemcpyAsync(d_cameras, cameras, count * 16384, hipMemcpyHostToDevice, s) ==
+            hipSuccess &&
+        tb_cuda_extract_features_device(d_obs, d_mission, d_cameras, d_features, count,
+                                        stream) &&
+        hipMemcpyAsync(out_features, d_features, count * kFeatureDim * sizeof(float),
+                       hipMemcpyDeviceToHost, s) == hipSuccess;
+    const bool done = hipStreamSynchronize(s) == hipSuccess;
+    if (!ok) (void)hipGetLastError();
+    return ok && done;
 }
 
 extern "C" int tb_hip_lidar_transform_device(const float *ranges, float *out, size_t count,

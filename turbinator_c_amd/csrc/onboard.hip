@@ -1519,9 +1519,11 @@ extern "C" int tb_hip_onboard_tactical_prior_device(const float *obs, const floa
 // scalars and mission values after their chains, and store tactical / prior
 // and their copies.  Fusing the scan into the streaming launch was measured
 // slower: next to saturated HBM traffic the scan's dependent loads stall.  Luma is
-// the reference's `(float)b * (1.0f / 255.0f) - 0.5f` with two roundings, as
-// C evaluates it (this file is built without FMA contraction, like every
-// restatement of the reference's arithmetic here).
+// the reference's `(float)b * (1.0f / 255.0f) - 0.5f` as its CUDA build
+// evaluates it: nvcc contracts the product and difference into one fused
+// multiply-add by default, so it is one explicit fma here (this file is built
+// without automatic contraction, like every restatement of the reference's
+// arithmetic here).
 
 namespace {
 
@@ -1601,7 +1603,8 @@ __global__ __launch_bounds__(kStreamThreads) void actor_stream_kernel(ActorRows 
                 f32x4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    o[e] = (float)((w >> (8 * e)) & 0xffu) * (1.0f / 255.0f) - 0.5f;
+                    o[e] = __builtin_fmaf((float)((w >> (8 * e)) & 0xffu), 1.0f / 255.0f,
+                                          -0.5f);
                 store_plane(dst, 16384 * 4, t + 1024 * k, o);
             }
         }
