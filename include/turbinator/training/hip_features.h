@@ -184,8 +184,11 @@ int tb_hip_actor_inputs_device(const float *obs, const float *mission,
  * act entry reads; packed_bytes returns 0 for a hidden width out of range.
  * The buffer holds each weight row scaled by a power of two and split into
  * two fp16 pieces for the fp16 matrix cores (products within about 7e-7 of
- * their fp32 value); weights must be finite: a non-finite weight makes its
- * output NaN for every row, where the reference's would be +-inf or NaN. */
+ * their fp32 value, plus up to 2^-39 of the row's largest magnitude times
+ * the other operand for an operand more than 2^28 below its row's largest,
+ * whose pieces are fp16 subnormals); weights must be finite: a non-finite
+ * weight makes its output NaN for every row, where the reference's would be
+ * +-inf or NaN. */
 size_t tb_hip_sac_actor_packed_bytes(int hidden);
 int tb_hip_sac_actor_pack_device(const float *w0, const float *b0, const float *w1,
                                  const float *b1, const float *w2, const float *b2,

@@ -3,17 +3,18 @@ parity tests (tests/test_gpu_sac_actor.py `conditioning`), checked on the CPU.
 
 J = sum over both hidden layers and units n of |d out / d p_n| S_n, where p_n
 is the unit's pre-activation and S_n = |b_n| + sum_k |w_nk x_k| the magnitude
-of its summands.  Its derivatives are hand-derived (tanh' = 1 - h^2 through
-the later layers); here they are compared with central differences of a
-float64 forward pass in which each pre-activation is perturbed on its own,
-so a transposed weight, a dropped tanh' or an absolute value taken inside
-the sum instead of outside fails.
+of its summands, plus the fp16 subnormal pieces' term (summand_scales).  Its
+derivatives are hand-derived (tanh' = 1 - h^2 through the later layers);
+here they are compared with central differences of a float64 forward pass in
+which each pre-activation is perturbed on its own, so a transposed weight, a
+dropped tanh' or an absolute value taken inside the sum instead of outside
+fails.
 """
 from __future__ import annotations
 
 import numpy as np
 
-from tests.test_gpu_sac_actor import conditioning, random_weights
+from tests.test_gpu_sac_actor import conditioning, random_weights, summand_scales
 
 HIDDEN = 8
 
@@ -40,10 +41,8 @@ def case(seed=3):
 
 def finite_difference_j(w, x, step=1e-6):
     xd = x.astype(np.float64)
-    w0, b0, w1, b1, _, _ = (np.asarray(a, np.float64) for a in w)
-    _, h0, _ = forward(w, xd)
-    s0 = np.abs(b0) + np.abs(xd) @ np.abs(w0).T
-    s1 = np.abs(b1) + np.abs(h0) @ np.abs(w1).T
+    _, h0, h1 = forward(w, xd)
+    s0, s1, _ = summand_scales(w, xd, h0, h1)
     j = np.zeros((x.shape[0], 30))
     for layer, s in ((0, s0), (1, s1)):
         for n in range(HIDDEN):
@@ -57,9 +56,9 @@ def finite_difference_j(w, x, step=1e-6):
 
 
 def last_layer_scale(w, x):
-    _, h1 = forward(w, x.astype(np.float64))[1:]
-    w2, b2 = np.asarray(w[4], np.float64), np.asarray(w[5], np.float64)
-    return np.abs(b2) + np.abs(h1) @ np.abs(w2).T
+    xd = x.astype(np.float64)
+    _, h0, h1 = forward(w, xd)
+    return summand_scales(w, xd, h0, h1)[2]
 
 
 def test_jacobian_term_matches_central_differences():
@@ -76,8 +75,7 @@ def test_absolute_values_inside_the_sum_fail():
     w0, b0, w1, b1, w2, b2 = (np.asarray(a, np.float64) for a in w)
     _, h0, h1 = forward(w, xd)
     g0, g1 = 1 - h0 * h0, 1 - h1 * h1
-    s0 = np.abs(b0) + np.abs(xd) @ np.abs(w0).T
-    s1 = np.abs(b1) + np.abs(h0) @ np.abs(w1).T
+    s0, s1, _ = summand_scales(w, xd, h0, h1)
     loose = ((g1 * s1) @ np.abs(w2).T
              + np.einsum("om,em,mn,en->eo", np.abs(w2), g1, np.abs(w1), g0 * s0))
     fd = finite_difference_j(w, x)

@@ -19,7 +19,12 @@ output is held to a bound set by its own conditioning:
     the network's own float64 derivatives.  A hidden unit far from
     saturation whose summands cancel (S_ln >> |p_ln|, as with features over
     ten decades against first-layer weights over ten more) passes the error
-    of its sum on to the output on both sides, the reference's included;
+    of its sum on to the output on both sides, the reference's included.
+    S_l also carries the fp16 subnormal pieces' absolute error (SUBNORMAL):
+    an operand more than 2^28 below its row's largest is rounded to fp16's
+    subnormal grid, an error of up to 2^-39 of that largest magnitude (and no
+    more than the operand itself), however small the operand's own product
+    (tests/test_split_products.py);
   * actions: (1 - a^2) dz + 2.4e-7, dz the raw bound of the mean plus the
     exp-rounding of std * eps (tanh' = 1 - a^2; 2.4e-7 = tanh rounding);
   * log-probability: 1e-4 (1 + |lp|) plus, per action, the log-std bound and
@@ -79,19 +84,52 @@ def run_gpu(torch, weights, hidden, feats, draws, want_raw=True):
 
 
 RAW_EPS = 1e-6
+# A scaled operand's piece below fp16's normal range (2^-14) is rounded to
+# the subnormal grid: an absolute error of at most 2^-25 at the row's scale,
+# which is 2^-39 of the row's largest magnitude (of 1 for hidden
+# activations, whose scale is a fixed 2^14), and never more than the value
+# itself.  It follows the row's largest magnitude rather than the product,
+# so when a row's largest weight meets a zero feature and a weight 2^30
+# below it meets a large one, that product carries an error far above
+# eps |w x|.
+SUBNORMAL = 2.0 ** -39
 
 
-def conditioning(weights, feats) -> np.ndarray:
+def summand_scales(weights, x, h0, h1, subnormal=True):
+    """S_l per (row, unit) of the three layers, in float64: |b| + sum_k |w_k x_k|,
+    plus (with `subnormal`) the subnormal pieces' absolute error in units of
+    RAW_EPS: sum_k |x_k| min(|w_k|, 2^-39 max|w|) + |w_k| min(|x_k|, 2^-39 max|x|),
+    max|x| = 1 for the hidden activations (tests/test_split_products.py holds
+    the two-piece split to this).  Infinite features have no pieces (the kernel
+    adds their products in fp32), so they count as 0 in that term."""
+    w0, b0, w1, b1, w2, b2 = (np.asarray(a, np.float64) for a in weights)
+    s0 = np.abs(b0) + np.abs(x) @ np.abs(w0).T
+    s1 = np.abs(b1) + np.abs(h0) @ np.abs(w1).T
+    s2 = np.abs(b2) + np.abs(h1) @ np.abs(w2).T
+    if subnormal:
+        def term(a, w, a_max):
+            aw = np.abs(w)
+            floor_w = np.minimum(aw, SUBNORMAL * aw.max(1, keepdims=True))
+            return (a @ floor_w.T + np.minimum(a, SUBNORMAL * a_max) @ aw.T) / RAW_EPS
+
+        ax = np.where(np.isfinite(x), np.abs(x), 0.0)
+        s0 = s0 + term(ax, w0, ax.max(1, keepdims=True))
+        s1 = s1 + term(np.abs(h0), w1, 1.0)
+        s2 = s2 + term(np.abs(h1), w2, 1.0)
+    return s0, s1, s2
+
+
+def conditioning(weights, feats, subnormal=True) -> np.ndarray:
     """1 + S2 + J per (row, output), in float64: S2 = |b2| + |h1| @ |w2|^T, and
-    J = sum_n |d out / d p0_n| S0_n + sum_m |d out / d p1_m| S1_m.  Units fed an
-    infinite feature are saturated (tanh' = 0) and contribute nothing."""
+    J = sum_n |d out / d p0_n| S0_n + sum_m |d out / d p1_m| S1_m, each S_l with
+    the subnormal pieces' term of summand_scales.  Units fed an infinite
+    feature are saturated (tanh' = 0) and contribute nothing."""
     w0, b0, w1, b1, w2, b2 = (np.asarray(x, np.float64) for x in weights)
     x = feats.astype(np.float64)
     with np.errstate(invalid="ignore", over="ignore"):
         h0 = np.tanh(x @ w0.T + b0)
         h1 = np.tanh(h0 @ w1.T + b1)
-        s0 = np.abs(b0) + np.abs(x) @ np.abs(w0).T
-        s1 = np.abs(b1) + np.abs(h0) @ np.abs(w1).T
+        s0, s1, s2 = summand_scales(weights, x, h0, h1, subnormal)
         g0, g1 = 1 - h0 * h0, 1 - h1 * h1
         # d out_o / d p1_m = w2[o, m] g1_m;  d out_o / d p0_n = sum_m w2[o, m] g1_m w1[m, n] g0_n
         t1 = (g1 * s1) @ np.abs(w2).T
@@ -100,17 +138,16 @@ def conditioning(weights, feats) -> np.ndarray:
         for r in range(0, len(x), 512):  # [rows, out, hidden] slabs of at most ~30 MB
             d0 = np.abs((w2[None] * g1[r:r + 512, None, :]) @ w1)
             t0[r:r + 512] = np.einsum("eon,en->eo", d0, s0g[r:r + 512])
-        s2 = np.abs(b2) + np.abs(h1) @ np.abs(w2).T
         out = 1 + s2 + t0 + t1
     return np.nan_to_num(out, nan=1.0, posinf=1.0)
 
 
-def check(got, want, weights, feats, draws, label):
+def check(got, want, weights, feats, draws, label, subnormal=True):
     (ga, glp, graw), (wa, wlp, wraw) = got, want
     scale = np.ones(15)
     scale[14] = 0.15
     eps = np.zeros(wa.shape) if draws is None else np.abs(draws * scale)
-    raw_tol = RAW_EPS * conditioning(weights, feats)
+    raw_tol = RAW_EPS * conditioning(weights, feats, subnormal)
     if graw is not None:
         finite = np.isfinite(wraw)
         assert np.array_equal(finite, np.isfinite(graw)), f"{label}: raw finiteness"
@@ -235,6 +272,42 @@ def test_wide_dynamic_range(torch_cuda, hip):
         got = run_gpu(torch_cuda, w, hidden, feats, d)
         stats = check(got, oracle.sac_actor(ow, feats, d), w, feats, d, "wide range")
         note(f"wide range {'det' if d is None else 'stoch'}: {stats}")
+
+
+def anticorrelated_case(seed: int = 31):
+    """First-layer rows whose largest weight (2^20) meets a zero feature while
+    a weight 2^30 .. 2^37 below it meets a feature of +-2^10: that weight's
+    scaled pieces are fp16 subnormals, rounded by up to 2^-25 at the row's
+    scale (2^-9 of the unit's pre-activation, which is about 2^-7 .. 1 here),
+    and the unit stays unsaturated, so the error reaches the outputs.  Units
+    0..15 are such rows; the rest keep random weights."""
+    hidden = 128
+    rng = np.random.default_rng(seed)
+    w = random_weights(hidden, seed=seed)
+    for n in range(16):
+        w[0][n] = 0.0
+        w[0][n, 0] = 2.0 ** 20
+        w[0][n, 1 + n] = np.float32((1.0 + rng.uniform(0.0, 0.99)) * 2.0 ** (-10 - (n % 8)))
+    feats = random_features(128, seed=seed + 1)
+    feats[:, 0] = 0.0
+    feats[:, 1:17] = rng.choice([-1.0, 1.0], (128, 16)) * 2.0 ** 10
+    return hidden, w, feats
+
+
+def test_anticorrelated_subnormal_pieces(torch_cuda, hip):
+    """The subnormal term is what holds these rows: without it the bound
+    fails on them, with it the outputs pass."""
+    note("sac actor anticorrelated rows, subnormal weight pieces, hidden 128")
+    hidden, w, feats = anticorrelated_case()
+    draws = np.random.default_rng(32).standard_normal((128, 15)).astype(np.float32)
+    ow = oracle.SacActorWeights(*w)
+    for d in (None, draws):
+        got = run_gpu(torch_cuda, w, hidden, feats, d)
+        want = oracle.sac_actor(ow, feats, d)
+        stats = check(got, want, w, feats, d, "anticorrelated")
+        with pytest.raises(AssertionError):
+            check(got, want, w, feats, d, "anticorrelated, no subnormal term", subnormal=False)
+        note(f"anticorrelated {'det' if d is None else 'stoch'}: {stats}")
 
 
 @pytest.mark.parametrize("batch", [1, 15, 63, 65, 16384])

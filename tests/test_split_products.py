@@ -82,3 +82,74 @@ def test_an_unscaled_operand_fails_the_bound():
     assert np.all(np.abs(three_terms(scaled(w), x) - scaled(w).astype(np.float64)
                          * x.astype(np.float64))
                   <= BOUND * np.abs(scaled(w).astype(np.float64) * x.astype(np.float64)))
+
+
+def scale_exponent(x: np.ndarray) -> int:
+    """The kernel's row exponent t: max |x| 2^t in [2^14, 2^15)."""
+    m = np.abs(x).max()
+    return 14 - (int(np.frexp(np.float64(m))[1]) - 1)
+
+
+def split_dot(w: np.ndarray, x: np.ndarray) -> float:
+    """sum_k w_k x_k as the kernel forms it from one weight row and one
+    feature row: each row scaled by its own power of two, split, the three
+    cross terms summed (exactly, in float64 here) and unscaled."""
+    tw, tx = scale_exponent(w), scale_exponent(x)
+    ws = np.ldexp(w.astype(np.float32), tw).astype(np.float32)
+    xs = np.ldexp(x.astype(np.float32), tx).astype(np.float32)
+    return float(np.ldexp(three_terms(ws, xs).sum(), -(tw + tx)))
+
+
+def subnormal_term(w: np.ndarray, x: np.ndarray) -> float:
+    """sum_k |x_k| min(|w_k|, 2^-39 max|w|) + |w_k| min(|x_k|, 2^-39 max|x|):
+    the absolute error the pieces' subnormal rounding may add to the sum."""
+    aw, ax = np.abs(w.astype(np.float64)), np.abs(x.astype(np.float64))
+    sub = 2.0 ** -39
+    return float((ax * np.minimum(aw, sub * aw.max())).sum()
+                 + (aw * np.minimum(ax, sub * ax.max())).sum())
+
+
+def test_an_anticorrelated_row_needs_the_subnormal_term():
+    """The row's largest weight (2^20) meets a zero feature and a weight 2^30
+    below it meets 2^10: at the row's scale that weight is an fp16
+    subnormal, and its rounding error is about 1e-3 of the sum, far above
+    any multiple of u sum|w x|, but within the subnormal term."""
+    w = np.array([2.0 ** 20, 1.23 * 2.0 ** -10], np.float32)
+    x = np.array([0.0, 2.0 ** 10], np.float32)
+    exact = float(w.astype(np.float64) @ x.astype(np.float64))
+    err = abs(split_dot(w, x) - exact)
+    assert err > 1e-4 * abs(exact)
+    assert err <= BOUND * abs(exact) + subnormal_term(w, x)
+
+
+def test_rows_across_the_float_range_within_the_two_terms():
+    """Dot products of one weight row and one feature row at random scales
+    (2^-30 .. 2^30), in both signs.  Even trials: both rows spread over
+    2^-50 .. 1 of their largest entry.  Odd trials, anticorrelated: one weight
+    dominates a row spread over 2^-45 .. 2^-20 of it (so most weights are
+    fp16 subnormals at the row's scale) and meets a zero feature, the other
+    features spread over 2^-10 .. 1.  Every sum is within 3 * 2^-22 sum|w x|
+    plus the subnormal term, and the anticorrelated ones need that term."""
+    rng = np.random.default_rng(5)
+    n = 142
+    needed = 0
+
+    def row(lo, hi):
+        return (rng.choice([-1.0, 1.0], n) * 2.0 ** rng.uniform(lo, hi, n)
+                * 2.0 ** rng.uniform(-30, 30))
+
+    for trial in range(2000):
+        if trial % 2 == 0:
+            w, x = row(-50, 0), row(-50, 0)
+        else:
+            w, x = row(-45, -20), row(-10, 0)
+            j = int(rng.integers(n))
+            w[j] = np.abs(w).max() * 2.0 ** 20
+            x[j] = 0.0
+        w, x = w.astype(np.float32), x.astype(np.float32)
+        exact = float(w.astype(np.float64) @ x.astype(np.float64))
+        mag = float(np.abs(w.astype(np.float64) * x.astype(np.float64)).sum())
+        err = abs(split_dot(w, x) - exact)
+        assert err <= BOUND * mag + subnormal_term(w, x)
+        needed += err > BOUND * mag
+    assert needed > 500

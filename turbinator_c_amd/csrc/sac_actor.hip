@@ -34,8 +34,14 @@
 // features while they are staged, and the hidden activations (tanh, at
 // most 1) by 2^14.  A piece more than 2^28 below its row's largest
 // magnitude is an fp16 subnormal, whose rounding (at most 2^-25 at that
-// scale) is below 2^-39 of the row's largest magnitude.  The sums are
-// unscaled with ldexp before the bias is added (exact: powers of two).
+// scale) is up to 2^-39 of the row's largest magnitude, and no more than the
+// operand.  That error follows the row's largest magnitude, not the
+// product: where a row's largest weight meets a zero feature and a weight
+// 2^30 below it meets a large one, it reaches about 1e-3 of the sum.  So a
+// sum's error is a few u sum|w x| plus sum_k |x_k| min(|w_k|, 2^-39 max|w|)
+// + |w_k| min(|x_k|, 2^-39 max|x|) (max|x| = 1 for hidden activations).
+// The sums are unscaled with ldexp before the bias is added (exact: powers
+// of two).
 //
 // The products are transposed, H^T = W * X^T, over groups of 16
 // environments: the weights are the A operand and the environments the
