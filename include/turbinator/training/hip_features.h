@@ -161,10 +161,11 @@ int tb_hip_onboard_tactical_prior_device(const float *obs, const float *mission,
  *   camera_luma  [batch, 16384] (nullable): byte / 255 - 0.5
  * obs, cameras, lidar_channels and camera_luma must be 16-byte aligned;
  * camera_luma needs cameras.  Returns 0 for NULL required pointers,
- * misalignment, batch 0 or above 0x7fffffff.  From 1,536 environments with a
+ * misalignment, batch 0 or above 0x7fffffff.  From 1,792 environments with a
  * plane output the scan and control kernels run on a second stream of the
  * device (made once, on first use), forked from `stream` and joined back to
- * it: later work on `stream` sees every output. */
+ * it: later work on `stream` sees every output.  Outputs do not depend on
+ * the batch size or on the stream mode. */
 int tb_hip_actor_inputs_device(const float *obs, const float *mission,
                                const unsigned char *cameras, float *proprio,
                                float *mission_vec, float *tactical, float *prior,

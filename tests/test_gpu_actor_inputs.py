@@ -155,6 +155,22 @@ def test_config_16384(torch_cuda, hip):
     check_h2(sub, want, "16384")
 
 
+@pytest.mark.parametrize("n", [300, 1024, 2048, 2560])
+def test_lidar_or_luma_alone(torch_cuda, hip, n):
+    """The scan kernel writes the channel planes of elevation rows 0..5 and
+    the plane kernel the other rows: each plane output requested alone, at a
+    one-stream batch and at one that overlaps the two streams, is complete
+    and bit-exact against numpy for every environment."""
+    note(f"actor inputs, lidar or luma alone, {n} envs")
+    b = synth.make_batch(n, seed=700 + n, threads=16)
+    got = run_actor(torch_cuda, hip, b.obs, b.mission, None, lidar=True, luma=False)
+    assert np.array_equal(u32(got["lidar"]), u32(numpy_lidar_channels(b.obs)))
+    check_copies(got, f"lidar{n}")
+    got = run_actor(torch_cuda, hip, b.obs, b.mission, b.cameras, lidar=False, luma=True)
+    assert np.array_equal(u32(got["luma"]), u32(exact_luma(b.cameras)))
+    check_copies(got, f"luma{n}")
+
+
 def _call_all(torch, hip, d_in, out, n, stream_arg, s_sync):
     assert hip.actor_inputs_device(*d_in, *out, n, stream_arg) == 1
     assert hip.synchronize(s_sync) == 1
@@ -169,30 +185,32 @@ def _device_batch(torch, n, seed):
     return d_in, out
 
 
-def test_overlap_threshold_and_null_stream(torch_cuda, hip):
-    """From 1,536 environments with plane outputs the scan and control
-    kernels run on a second stream beside the plane kernel.  The 1,536-row
-    call must equal the 1,535-row call (one stream) on their common rows, bit
-    for bit, and a call on the null stream must equal one on a torch stream."""
+def test_mode_thresholds_and_null_stream(torch_cuda, hip):
+    """The entry picks its mode by batch: one stream below 1,792
+    environments, with the scan kernel writing its rows' LiDAR channels from
+    512; two streams from 1,792, with that split from 2,560.  Every call on
+    either side of each threshold must equal the 2,560-row call on their
+    common rows, bit for bit, and a call on the null stream must equal one on
+    a torch stream."""
     torch = torch_cuda
-    note("actor inputs: overlap threshold 1535 / 1536, null stream")
-    d_in, out = _device_batch(torch, 1536, seed=1536)
+    names = ("proprio", "mission", "tactical", "prior", "lidar", "luma")
+    note("actor inputs: mode thresholds 512 / 1792 / 2560, null stream")
+    d_in, out = _device_batch(torch, 2560, seed=2560)
     s = torch.cuda.current_stream()
     torch.cuda.synchronize()
-    two_streams = _call_all(torch, hip, d_in, out, 1536, s, s)
+    full = _call_all(torch, hip, d_in, out, 2560, s, s)
+    for n in (511, 512, 1791, 1792, 2559):
+        for t in out:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        part = _call_all(torch, hip, d_in, out, n, s, s)
+        for name, g, w in zip(names, full, part):
+            assert np.array_equal(g[:n], w), f"{name}: {n}-row call differs from 2560-row call"
     for t in out:
         t.fill_(float("nan"))
     torch.cuda.synchronize()
-    one_stream = _call_all(torch, hip, d_in, out, 1535, s, s)
-    for name, g, w in zip(("proprio", "mission", "tactical", "prior", "lidar", "luma"),
-                          two_streams, one_stream):
-        assert np.array_equal(g[:1535], w), f"{name}: 1536-row call differs from 1535-row call"
-    for t in out:
-        t.fill_(float("nan"))
-    torch.cuda.synchronize()
-    null = _call_all(torch, hip, d_in, out, 1536, None, None)
-    for name, g, w in zip(("proprio", "mission", "tactical", "prior", "lidar", "luma"),
-                          null, two_streams):
+    null = _call_all(torch, hip, d_in, out, 2560, None, None)
+    for name, g, w in zip(names, null, full):
         assert np.array_equal(g, w), f"{name}: null-stream call differs"
 
 
@@ -273,8 +291,9 @@ def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
     environments (the scan waves form a second group of 64 frames, and the
     control kernel's workgroups, which also write the symlog scalars, loop
     past their 4,096-workgroup cap); proprio, mission, tactical and prior
-    rows must equal the 4,096-row call's bit for bit.  The plane outputs are
-    left out (they do not depend on the scan)."""
+    rows must equal the 4,096-row call's bit for bit, and so must the LiDAR
+    channels (the scan waves write those of their rays), compared on the
+    device.  Luma is left out (no scan wave writes it)."""
     torch = torch_cuda
     distinct, batch = 4096, 64 * 4096 + 1000
     note(f"actor inputs {batch} envs tiled from {distinct}")
@@ -287,20 +306,25 @@ def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
         n = o.shape[0]
         out = [torch.full((n, w), float("nan"), dtype=torch.float32, device="cuda")
                for w in (91, 49, 24, 15)]
+        lidar = torch.full((n, 6, 16, 128), float("nan"), dtype=torch.float32, device="cuda")
         s = torch.cuda.current_stream()
-        assert hip.actor_inputs_device(o, m, None, *out, None, None, n, s) == 1
+        assert hip.actor_inputs_device(o, m, None, *out, lidar, None, n, s) == 1
         assert hip.synchronize(s) == 1
-        return [t.cpu().numpy().view(np.uint32) for t in out]
+        return [t.cpu().numpy().view(np.uint32) for t in out], lidar
 
-    small = run(obs, mission)
+    small, small_lidar = run(obs, mission)
     big_obs = obs.repeat(reps, 1)[:batch].contiguous()
     big_mis = mission.repeat(reps, 1)[:batch].contiguous()
-    big = run(big_obs, big_mis)
+    big, big_lidar = run(big_obs, big_mis)
     del big_obs, big_mis
     rows = np.arange(batch) % distinct
     for g, w, name in zip(big, small, ("proprio", "mission", "tactical", "prior")):
         bad = np.argwhere((g != w[rows]).any(1)).ravel()
         assert not bad.size, f"{name} differs at rows {bad[:5]}"
+    for k in range(reps):
+        n = min(distinct, batch - k * distinct)
+        assert torch.equal(big_lidar[k * distinct:k * distinct + n].view(torch.int32),
+                           small_lidar[:n].view(torch.int32)), f"lidar differs in tile {k}"
 
 
 def test_argument_validation(hip):

@@ -15,6 +15,11 @@
   eight k values) before it rounds the sum, and over random blocks its error
   stays within a few u sum|p| (tests/csrc/check_mfma_sum.hip): the compact
   actor's error analysis and its conditioned parity bound rest on this.
+* recip_range(y), the hardware reciprocal refined by one Newton step, is
+  the IEEE quotient 1.0f / y for every float y in [0.2, 30]
+  (tests/csrc/check_recip.hip, all 61,027,124 of them): the 618M actor's
+  inverse-range channel (network_gpu.cu:467-479) divides by a value in that
+  range, so its bits equal the reference's correctly rounded division.
 """
 from __future__ import annotations
 
@@ -69,3 +74,15 @@ def test_mfma_block_sum_drops_low_product_bits():
     # not the correctly rounded sum: some results lie below the nearest float
     assert truncated > 0 and above > 0, proc.stdout
     assert outputs == 262144 and worst <= 6.0 and mean <= 1.0, proc.stdout
+
+
+@pytest.mark.gpu
+def test_range_reciprocal_is_the_ieee_quotient():
+    exe = BIN / "check_recip"
+    if not exe.exists():
+        pytest.fail(f"{exe} is not built (run __graft_entry__.build())")
+    proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    w = proc.stdout.split()
+    assert int(w[0]) == 0x41F00000 - 0x3E4CCCCD + 1, proc.stdout
+    assert w[2] == "0" and w[8] == "0", proc.stdout

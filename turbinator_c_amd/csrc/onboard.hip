@@ -49,6 +49,7 @@
 #include <mutex>
 
 #include "turbinator/training/hip_features.h"
+#include "recip_range.h"
 #include "xcd_order.h"
 
 #include "onboard_rays.inc"
@@ -282,6 +283,24 @@ __device__ __forceinline__ unsigned window_offset(float range) {
     return __float_as_uint(range) - kWindowLo;
 }
 
+// The 618M actor's three LiDAR channels of one range (network_gpu.cu:
+// 467-479): inverse range, range / 30 and validity.  Both the plane kernel
+// and the scan kernel of the actor entry form them here.  The divisor of the
+// inverse range lies in [0.2, 30] for every input (non-finite ranges clamp
+// to 0.05 or 30), where recip_range is the IEEE quotient; it is formed on
+// every lane and selected, without a branch.
+__device__ __forceinline__ float lidar_channel(float range, int kind) {
+    const bool valid = range > 0.0f && __builtin_isfinite(range);
+    const float clamped = fmaxf(0.05f, fminf(30.0f, range));
+    if (kind == 0) return valid ? recip_range(fmaxf(0.2f, clamped)) : 0.0f;
+    if (kind == 1) return valid ? div_const(clamped, 30.0f) : 1.0f;
+    return valid ? 1.0f : 0.0f;
+}
+
+// Buffer cache-policy bits of the actor entry's plane stores: nt (1) and
+// sc1 (4).
+constexpr int kStorePolicy = 2 | 16;
+
 // onboard_features.cuh:199-207 for one ray with rotated direction rw:
 // returns the corridor centre x (+inf when the ray is outside the window or
 // the corridor) and sets y_center.  Bitwise, so the compares stay one
@@ -336,9 +355,30 @@ __device__ __forceinline__ float add_in_lane_order(float sum, float v, uint64_t 
 //     registers take the next environment's (`next`, a 0-byte resource when
 //     there is none): they have the rest of this environment to arrive.
 //   * `f` is wave-uniform.
+//   * With PLANES (the 618M actor's entry) the wave first writes the three
+//     LiDAR channel planes of its 1,536 rays into `planes`, the
+//     environment's [6][16][128] channel block: these rays are in its
+//     registers already, so the entry reads them from HBM once, and the
+//     plane kernel writes only the other elevation rows.
+template <bool PLANES>
 __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes &rays,
                                          const ScanFrame &f, __amdgpu_buffer_rsrc_t next,
-                                         int lane, u32x2 *list, ScanResult &out) {
+                                         __amdgpu_buffer_rsrc_t planes, int lane, u32x2 *list,
+                                         ScanResult &out) {
+    if (PLANES) {
+        // Slot u holds row 6 head + el, azimuths 64 (u % 2) + lane: channel
+        // kind k of head h is plane h + 2k, so each store writes 256
+        // consecutive bytes of one plane row.
+#pragma unroll
+        for (int u = 0; u < kScanRays; ++u) {
+            const int row = u / 2, head = row / 6, el = row % 6;
+#pragma unroll
+            for (int kind = 0; kind < 3; ++kind)
+                __builtin_amdgcn_raw_buffer_store_b32(
+                    __builtin_bit_cast(unsigned, lidar_channel(rg[u], kind)), planes, 4 * lane,
+                    4 * ((head + 2 * kind) * 2048 + el * 128 + 64 * (u % 2)), kStorePolicy);
+        }
+    }
     // List the in-window rays in slot order while counting them: entry =
     // (range bits - kWindowLo, ray).  The slot's first entry address is
     // uniform (scalar), so each lane's address is one shift-add of its lane
@@ -1119,6 +1159,7 @@ struct OnboardRows {
     float *diag;
     float *proprio;      // optional [batch, 91]: tactical -> 52..75, prior -> 76..90
     float *mission_vec;  // optional [batch, 49]: tactical -> 10..33, prior -> 34..48
+    float *lidar;        // optional [batch, 6, 16, 128]: channels of the scan rays
     size_t batch;
 };
 
@@ -1184,6 +1225,7 @@ __device__ __forceinline__ void actor_scalars(float raw, int lane, float *propri
 // 32-byte result is parked in the environment's own prior row (60 bytes),
 // which phase 2 reads before it writes the 15 prior values there: no
 // scratch memory is needed.
+template <bool PLANES>
 __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows rows) {
     __shared__ RayPlanes rays;
     __shared__ u32x2 lists[kWavesPerBlock][kListCap + 64];  // + a spare entry per lane
@@ -1221,8 +1263,11 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
         const size_t next_env = env + waves;
         const bool has_next = next_env < rows.batch;
         ScanResult s;
-        scan_env(rg, rays, f, obs_rsrc(has_next ? obs_of(next_env) : nullptr, has_next), lane,
-                 lists[__builtin_amdgcn_readfirstlane(tid >> 6)], s);
+        const __amdgpu_buffer_rsrc_t planes = __builtin_amdgcn_make_buffer_rsrc(
+            PLANES ? rows.lidar + env * 12288 : nullptr, (short)0, PLANES ? 12288 * 4 : 0,
+            kBufferWord3);
+        scan_env<PLANES>(rg, rays, f, obs_rsrc(has_next ? obs_of(next_env) : nullptr, has_next),
+                         planes, lane, lists[__builtin_amdgcn_readfirstlane(tid >> 6)], s);
         if (lane == 0) {
             float *park = rows.prior + env * 15;
             park[0] = s.min_r;
@@ -1476,7 +1521,10 @@ int launch_onboard(const OnboardRows &rows, hipStream_t s) {
     const size_t scan_want = (rows.batch + kWavesPerBlock - 1) / kWavesPerBlock;
     const unsigned scan_blocks = scan_want > kScanBlocks ? kScanBlocks : (unsigned)scan_want;
     const size_t ctrl_want = (rows.batch + 63) / 64;
-    onboard_scan_kernel<<<scan_blocks, kBlockThreads, 0, s>>>(rows);
+    if (rows.lidar)
+        onboard_scan_kernel<true><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
+    else
+        onboard_scan_kernel<false><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
     const unsigned ctrl_blocks = ctrl_want > kControlBlocks ? kControlBlocks : (unsigned)ctrl_want;
     if (rows.proprio)
         onboard_control_kernel<true><<<ctrl_blocks, kControlThreads, 0, s>>>(rows);
@@ -1502,6 +1550,7 @@ extern "C" int tb_hip_onboard_tactical_prior_device(const float *obs, const floa
     rows.diag = diag;
     rows.proprio = nullptr;
     rows.mission_vec = nullptr;
+    rows.lidar = nullptr;
     rows.batch = batch_size;
     (void)hipGetLastError();
     return launch_onboard(rows, reinterpret_cast<hipStream_t>(stream));
@@ -1514,7 +1563,10 @@ extern "C" int tb_hip_onboard_tactical_prior_device(const float *obs, const floa
 // per environment streams the LiDAR block once into the six channel planes
 // and the cameras once into luma: LiDAR in 16-byte loads, camera bytes in
 // 4-byte loads so that each lane's 4 luma values are one float4 and every
-// store instruction writes 1 KiB of consecutive output.
+// store instruction writes 1 KiB of consecutive output.  From the split
+// threshold on, the scan kernel writes the channels of the rays it reads
+// (elevation rows 0..5) and this kernel only those of rows 6..15, so each
+// LiDAR range is read from HBM once.
 // The control kernel's controller waves add each environment's 52 symlog
 // scalars and mission values after their chains, and store tactical / prior
 // and their copies.  Fusing the scan into the streaming launch was measured
@@ -1530,25 +1582,22 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kStorePolicy = 2 | 16;  // buffer cache-policy bits: nt (1) and sc1 (4)
+// Threads of a head whose LiDAR float4 lies in the scan's elevation rows
+// 0..5 (6 rows of 32 float4).
+constexpr int kScanRowThreads = 6 * 128 / 4;
 
 struct ActorRows {
     const float *obs;
     const unsigned char *cameras;
     float *lidar, *luma;
     size_t batch;
+    bool scan_rows;  // also the channels of the scan rows (else the scan kernel writes them)
 };
 
 __device__ __forceinline__ f32x4 lidar_channel4(f32x4 r, int kind) {
     f32x4 o;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float range = r[e];
-        const bool valid = range > 0.0f && __builtin_isfinite(range);
-        const float clamped = fmaxf(0.05f, fminf(30.0f, range));
-        o[e] = kind == 0 ? (valid ? 1.0f / fmaxf(0.2f, clamped) : 0.0f)
-                         : (kind == 1 ? (valid ? div_const(clamped, 30.0f) : 1.0f) : (valid ? 1.0f : 0.0f));
-    }
+    for (int e = 0; e < 4; ++e) o[e] = lidar_channel(r[e], kind);
     return o;
 }
 
@@ -1576,8 +1625,13 @@ __global__ __launch_bounds__(kStreamThreads) void actor_stream_kernel(ActorRows 
     const int t = threadIdx.x;
     for (size_t env = xcd_contiguous(blockIdx.x, gridDim.x); env < rows.batch;
          env += gridDim.x) {
+        // float4 t is bins 4(t%512).. of head t/512, elevation row
+        // (t%512)/32.  Unless `scan_rows`, the scan kernel writes rows 0..5
+        // (threads with t%512 < 192, whole waves) and this kernel the other
+        // ten.
+        const bool lidar = rows.lidar && (rows.scan_rows || (t & 511) >= kScanRowThreads);
         f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (rows.lidar)
+        if (lidar)
             v = __builtin_nontemporal_load(
                 reinterpret_cast<const f32x4 *>(rows.obs + env * 4148 + 48) + t);
         unsigned px[4];
@@ -1586,9 +1640,8 @@ __global__ __launch_bounds__(kStreamThreads) void actor_stream_kernel(ActorRows 
 #pragma unroll
             for (int k = 0; k < 4; ++k) px[k] = __builtin_nontemporal_load(cam + t + 1024 * k);
         }
-        if (rows.lidar) {
-            // float4 t is bins 4(t%512).. of head t/512; head h feeds
-            // channels h, h+2, h+4.
+        if (lidar) {
+            // Head h feeds channels h, h+2, h+4.
             float *dst = rows.lidar + env * 12288;
             const int head = t >> 9, q = t & 511;
 #pragma unroll
@@ -1615,14 +1668,34 @@ __global__ __launch_bounds__(kStreamThreads) void actor_stream_kernel(ActorRows 
 // stream of the device, forked from and joined back to the caller's stream.
 // The plane kernel is write-bound and keeps one workgroup per CU; the scan
 // and control workgroups fit beside it, and their latency-bound chains
-// overlap its streams.  Measured on the entry (identical outputs): 77.8 ->
-// 68.3 us at 2,048 environments, 128.7 -> 118.4 at 4,096, 230.2 -> 222.6 at
-// 8,192 and 433.4 -> 428.6 at 16,384, 61.7 -> 59.4 at 1,536; the fork and
-// join cost about 19 us at 32 environments, 6.5 us at 1,024 and 2.7 us at
-// 1,280, so smaller batches keep one stream.  The scan alone on the second stream,
-// with the controller after the join, measured 437.9 us: it is the
-// controller that gains from running beside the planes.
-constexpr size_t kOverlapMinBatch = 1536;
+// overlap its streams.  It is the controller that gains most: the scan alone
+// on the second stream, with the controller after the join, measured 437.9
+// against 433.0 us at 16,384 environments (before the split below).
+//
+// Split of the LiDAR channel planes: from kSplitMinBatch environments the
+// scan kernel writes the channels of the 1,536 rays it reads (elevation rows
+// 0..5 of each head) and the plane kernel only the other rows, so the entry
+// reads every LiDAR range from HBM once instead of reading the scan rows
+// twice.  Measured on the entry (one box, outputs bit-equal in every mode;
+// one stream without / with the split, two streams without / with it):
+//    batch    one stream     two streams
+//      256    25.1 / 26.3    41.7 / 44.1
+//      512    32.0 / 31.0    45.6 / 45.7
+//    1,536    59.7 / 55.8    58.5 / 63.0
+//    1,792    65.4 / 62.9    62.7 / 66.5
+//    2,048    76.3 / 70.8    67.8 / 70.4
+//    2,432    88.8 / 86.8    73.7 / 75.4
+//    2,560    88.8 / 86.6    81.2 / 80.2
+//    4,096   128.9 / 123.6  124.1 / 111.7
+//    8,192   230.4 / 222.9  225.3 / 214.5
+//   16,384       --          428.5 / 412.5
+// So batches below kOverlapMinBatch keep one stream (the fork and join cost
+// several microseconds), with the split from kSplitMinBatch; from
+// kOverlapMinBatch two streams, with the split from kSplitOverlapMinBatch
+// (below it the longer scan holds up the second stream).
+constexpr size_t kSplitMinBatch = 512;
+constexpr size_t kSplitOverlapMinBatch = 2560;
+constexpr size_t kOverlapMinBatch = 1792;
 constexpr int kMaxDevices = 64;
 
 struct SideStream {
@@ -1688,6 +1761,8 @@ extern "C" int tb_hip_actor_inputs_device(const float *obs, const float *mission
     (void)hipGetLastError();
     const bool planes = lidar_channels || camera_luma;
     SideStream *side = planes && batch_size >= kOverlapMinBatch ? side_stream(s) : nullptr;
+    const bool split = lidar_channels && batch_size >= kSplitMinBatch &&
+                       (!side || batch_size >= kSplitOverlapMinBatch);
     std::unique_lock<std::mutex> order;
     if (side) {
         order = std::unique_lock<std::mutex>(side->order);
@@ -1702,6 +1777,7 @@ extern "C" int tb_hip_actor_inputs_device(const float *obs, const float *mission
         ar.lidar = lidar_channels;
         ar.luma = camera_luma;
         ar.batch = batch_size;
+        ar.scan_rows = !split;
         // One workgroup per CU: the launch asks for more than half of the
         // CU's 160 KB of LDS, which the kernel does not use (by registers a
         // CU holds two; one measured 462.7 -> 445.0 us for the entry,
@@ -1721,6 +1797,7 @@ extern "C" int tb_hip_actor_inputs_device(const float *obs, const float *mission
     rows.diag = nullptr;
     rows.proprio = proprio;
     rows.mission_vec = mission_vec;
+    rows.lidar = split ? lidar_channels : nullptr;
     rows.batch = batch_size;
     if (!side) return launch_onboard(rows, s);
     const int ok = launch_onboard(rows, side->stream);
