@@ -25,9 +25,8 @@
 //     slalom lane;
 //   * the tactical features and the controller (mission decode, targets,
 //     landing / standard / inversion / BWB laws, cannon) run in a second
-//     kernel from the parked scan results: one lane per environment for the
-//     tactical features, one quad of lanes per environment for the
-//     controller (lane a evaluates arm a and a quarter of the independent
+//     kernel from the parked scan results, both on one quad of lanes per
+//     environment (lane a evaluates arm a and a quarter of the independent
 //     transcendental calls).  The controller's long register-heavy chain is
 //     kept apart from the scan so both keep their occupancy.  The angles
 //     that reach its angle wraps use a correctly rounded atan2: exact angles
@@ -58,7 +57,8 @@ namespace {
 
 constexpr int kBlockThreads = 256;
 constexpr int kWavesPerBlock = kBlockThreads / 64;
-constexpr int kControlThreads = 320;  // wave 0 tactical, waves 1..4 controller
+constexpr int kControlWaves = 4;  // control workgroup: waves 0..3 controller, 4..7 tactical
+constexpr int kControlThreads = 2 * kControlWaves * 64;
 constexpr int kScanRays = 1536 / 64;  // rays per lane: one wave scans one environment
 // In-window rays a wave lists for the compact pass; with more, every slot is
 // swept instead.
@@ -593,76 +593,6 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
     }
 }
 
-// onboard_features.cuh:25-86
-__device__ void tactical_features(const float *o, const float *m, float *t) {
-    const float pi = kPi;
-    float spool[4], fz[4], tau_z = 0.0f, spool_mean = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        spool[i] = ob_clamp(o[16 + i], 0.0f, 1.0f);
-        const float thrust = 0.036f + 0.964f * spool[i];
-        const float ci = cosf(o[28 + i]);
-        fz[i] = thrust * o[24 + i] * ci;
-        tau_z += thrust * o[20 + i] * ci;
-        spool_mean += spool[i];
-    }
-    spool_mean *= 0.25f;
-    float v[24];
-    v[0] = fz[1] - fz[3];
-    v[1] = fz[2] - fz[0];
-    v[2] = 0.5f * tau_z;
-    v[3] = 0.25f * (fz[0] + fz[1] + fz[2] + fz[3]) - 0.5f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[4 + i] = 2.0f * (spool[i] - spool_mean);
-    const float qw = o[6], qx = o[7], qy = o[8], qz = o[9];
-    const float bz_x = 2.0f * (qx * qz + qw * qy);
-    const float bz_y = 2.0f * (qy * qz - qw * qx);
-    const float ct = ob_clamp(1.0f - 2.0f * (qx * qx + qy * qy), -1.0f, 1.0f);
-    const float bx_x = 1.0f - 2.0f * (qy * qy + qz * qz);
-    const float bx_y = 2.0f * (qx * qy + qw * qz);
-    const float yaw = atan2f(bx_y, bx_x);
-    const SinCos yaw_sc = sin_cos(yaw);
-    const float cy = yaw_sc.c, sy = yaw_sc.s;
-    v[8] = cy * bz_y - sy * bz_x;
-    v[9] = -sy * bz_y - cy * bz_x;
-    v[10] = ct;
-    v[11] = ct < 0.20f ? 1.0f : 0.0f;
-    const float rx = atanhf(ob_clamp(m[7], -0.995f, 0.995f)) * 20.0f;
-    const float ry = atanhf(ob_clamp(m[8], -0.995f, 0.995f)) * 20.0f;
-    const float rz = atanhf(ob_clamp(m[9], -0.995f, 0.995f)) * 20.0f;
-    v[12] = tanhf((cy * rx + sy * ry) * 0.08f);
-    v[13] = tanhf((-sy * rx + cy * ry) * 0.08f);
-    v[14] = tanhf(rz * 0.12f);
-    v[15] = tanhf(hypotf(rx, ry) * 0.05f);
-    v[16] = tanhf((cy * o[3] + sy * o[4]) * 0.15f);
-    v[17] = tanhf((-sy * o[3] + cy * o[4]) * 0.15f);
-    v[18] = expf(-fmaxf(o[2] - 0.62f, 0.0f));
-    const float dist = fmaxf(ob_norm3(rx, ry, rz), 1.0f);
-    const float flight = div_const(dist, 20.0f);
-    const float wx = rx - o[3] * 0.5f * flight;
-    const float wy = ry - o[4] * 0.5f * flight;
-    const float wz = rz - o[5] * 0.5f * flight + 0.5f * 9.80665f * flight * flight;
-    const float ux = -qx, uy = -qy, uz = -qz;
-    const float cx = uy * wz - uz * wy + qw * wx;
-    const float cyq = uz * wx - ux * wz + qw * wy;
-    const float cz = ux * wy - uy * wx + qw * wz;
-    const float bx = wx + 2.0f * (uy * cz - uz * cyq);
-    const float by = wy + 2.0f * (uz * cx - ux * cz);
-    const float bz = wz + 2.0f * (ux * cyq - uy * cx);
-    const float az = ob_clamp(atan2f(by, bx), pi / 12.0f, pi * 5.0f / 12.0f);
-    const float el = ob_clamp(atan2f(bz, fmaxf(hypotf(bx, by), 0.2f)), -pi / 6.0f, pi / 6.0f);
-    const float err = hypotf(az - o[44], el - o[45]);
-    v[19] = div_const(az - pi * 0.25f, pi / 6.0f);
-    v[20] = div_const(el, pi / 6.0f);
-    v[21] = tanhf(err * 2.0f);
-    v[22] = (o[46] <= 0.02f && o[47] > 0.01f && err < 0.26f && dist < 34.0f) ? 1.0f : -1.0f;
-    v[23] = sinf(atan2f(ry, rx) - pi * 0.25f - yaw);
-#pragma unroll
-    for (int i = 0; i < 24; ++i)
-        t[i] = __builtin_isnan(v[i]) ? 0.0f
-                                     : (__builtin_isinf(v[i]) ? copysignf(1.0f, v[i]) : v[i]);
-}
-
 // Lane k of every group of four (a quad) reads quad lane K's value.
 template <int K>
 __device__ __forceinline__ float quad_lane(float v) {
@@ -680,6 +610,99 @@ __device__ __forceinline__ Quad4 quad_all(float v) {
 // Quad lane a's choice among four values.
 __device__ __forceinline__ float quad_pick(int a, float v0, float v1, float v2, float v3) {
     return a == 0 ? v0 : (a == 1 ? v1 : (a == 2 ? v2 : v3));
+}
+
+// onboard_features.cuh:25-86 on the four lanes of a quad: lane a evaluates
+// arm a's thrust terms, and the independent calls of one function are spread
+// over the quad and broadcast (the three atanhf of the mission offsets; yaw
+// and the target bearing; the two hypotf and the two atan2f of the aim;
+// eight tanhf in two calls), so a lane makes 11 library calls instead of
+// the 25 of the per-environment chain.  Every call takes the arguments the
+// reference's code gives it, and the arm sums are formed in its order from
+// the broadcasts, so each feature is the value that code forms.  Lane a
+// returns features 6a .. 6a + 5 in t, mapped as the reference maps them
+// (NaN -> 0, +-inf -> +-1).
+__device__ void tactical_quad(const float *o, const float *m, int a, float (&t)[6]) {
+    const float pi = kPi;
+    const float spool_a = ob_clamp(o[16 + a], 0.0f, 1.0f);
+    const float thrust_a = 0.036f + 0.964f * spool_a;
+    const float ci_a = cosf(o[28 + a]);
+    const Quad4 spool = quad_all(spool_a);
+    const Quad4 fz = quad_all(thrust_a * o[24 + a] * ci_a);
+    const Quad4 tz = quad_all(thrust_a * o[20 + a] * ci_a);
+    float tau_z = 0.0f, spool_mean = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        tau_z += tz.v[i];
+        spool_mean += spool.v[i];
+    }
+    spool_mean *= 0.25f;
+    float v[24];
+    v[0] = fz.v[1] - fz.v[3];
+    v[1] = fz.v[2] - fz.v[0];
+    v[2] = 0.5f * tau_z;
+    v[3] = 0.25f * (fz.v[0] + fz.v[1] + fz.v[2] + fz.v[3]) - 0.5f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[4 + i] = 2.0f * (spool.v[i] - spool_mean);
+    const float qw = o[6], qx = o[7], qy = o[8], qz = o[9];
+    const float bz_x = 2.0f * (qx * qz + qw * qy);
+    const float bz_y = 2.0f * (qy * qz - qw * qx);
+    const float ct = ob_clamp(1.0f - 2.0f * (qx * qx + qy * qy), -1.0f, 1.0f);
+    const float bx_x = 1.0f - 2.0f * (qy * qy + qz * qz);
+    const float bx_y = 2.0f * (qx * qy + qw * qz);
+    // rx, ry, rz on lanes 0, 1, 2 (lane 3 repeats rz).
+    const float r_a = atanhf(ob_clamp(m[7 + (a < 2 ? a : 2)], -0.995f, 0.995f)) * 20.0f;
+    const float rx = quad_lane<0>(r_a), ry = quad_lane<1>(r_a), rz = quad_lane<2>(r_a);
+    // yaw on lane 0, the target bearing atan2f(ry, rx) on the others.
+    const float at_a = atan2f(a == 0 ? bx_y : ry, a == 0 ? bx_x : rx);
+    const float yaw = quad_lane<0>(at_a), bearing = quad_lane<1>(at_a);
+    const SinCos yaw_sc = sin_cos(yaw);
+    const float cy = yaw_sc.c, sy = yaw_sc.s;
+    v[8] = cy * bz_y - sy * bz_x;
+    v[9] = -sy * bz_y - cy * bz_x;
+    v[10] = ct;
+    v[11] = ct < 0.20f ? 1.0f : 0.0f;
+    const float dist = fmaxf(ob_norm3(rx, ry, rz), 1.0f);
+    const float flight = div_const(dist, 20.0f);
+    const float wx = rx - o[3] * 0.5f * flight;
+    const float wy = ry - o[4] * 0.5f * flight;
+    const float wz = rz - o[5] * 0.5f * flight + 0.5f * 9.80665f * flight * flight;
+    const float ux = -qx, uy = -qy, uz = -qz;
+    const float cx = uy * wz - uz * wy + qw * wx;
+    const float cyq = uz * wx - ux * wz + qw * wy;
+    const float cz = ux * wy - uy * wx + qw * wz;
+    const float bx = wx + 2.0f * (uy * cz - uz * cyq);
+    const float by = wy + 2.0f * (uz * cx - ux * cz);
+    const float bz = wz + 2.0f * (ux * cyq - uy * cx);
+    // hypotf(rx, ry) on lane 0, hypotf(bx, by) on the others; then the aim's
+    // azimuth on lane 0 and elevation on the others.
+    const float hy_a = hypotf(a == 0 ? rx : bx, a == 0 ? ry : by);
+    const float h_rxy = quad_lane<0>(hy_a), h_bxy = quad_lane<1>(hy_a);
+    const float aim_a = atan2f(a == 0 ? by : bz, a == 0 ? bx : fmaxf(h_bxy, 0.2f));
+    const float az = ob_clamp(quad_lane<0>(aim_a), pi / 12.0f, pi * 5.0f / 12.0f);
+    const float el = ob_clamp(quad_lane<1>(aim_a), -pi / 6.0f, pi / 6.0f);
+    const float err = hypotf(az - o[44], el - o[45]);
+    const float th1 = tanhf(quad_pick(a, (cy * rx + sy * ry) * 0.08f, (-sy * rx + cy * ry) * 0.08f,
+                                      rz * 0.12f, h_rxy * 0.05f));
+    const float th2 = tanhf(quad_pick(a, (cy * o[3] + sy * o[4]) * 0.15f,
+                                      (-sy * o[3] + cy * o[4]) * 0.15f, err * 2.0f, 0.0f));
+    v[12] = quad_lane<0>(th1);
+    v[13] = quad_lane<1>(th1);
+    v[14] = quad_lane<2>(th1);
+    v[15] = quad_lane<3>(th1);
+    v[16] = quad_lane<0>(th2);
+    v[17] = quad_lane<1>(th2);
+    v[21] = quad_lane<2>(th2);
+    v[18] = expf(-fmaxf(o[2] - 0.62f, 0.0f));
+    v[19] = div_const(az - pi * 0.25f, pi / 6.0f);
+    v[20] = div_const(el, pi / 6.0f);
+    v[22] = (o[46] <= 0.02f && o[47] > 0.01f && err < 0.26f && dist < 34.0f) ? 1.0f : -1.0f;
+    v[23] = sinf(bearing - pi * 0.25f - yaw);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        const float x = quad_pick(a, v[k], v[6 + k], v[12 + k], v[18 + k]);
+        t[k] = __builtin_isnan(x) ? 0.0f : (__builtin_isinf(x) ? copysignf(1.0f, x) : x);
+    }
 }
 
 // One lane's share of the prior features: its arm's throttle, outer and
@@ -1299,15 +1322,15 @@ struct ControlStage {
 };
 
 // Phase 2: the tactical features and the controller, from the parked scan
-// result.  A workgroup covers 64 environments: wave 0 runs the tactical
-// features, one lane per environment; waves 1..4 run the controller, one
-// quad of lanes per environment (16 per wave), lane a of the quad on arm a.
+// result.  A workgroup covers 64 environments: waves 0..3 run the
+// controller and waves 4..7 the tactical features, each on one quad of lanes
+// per environment (16 per wave), so every SIMD holds one wave of each.
 // Both are long scalar chains and few waves exist per launch, so splitting
 // the work shortens the chains and spreads them over more SIMDs.  For the
-// actor's inputs (SCALARS) each controller wave then writes the symlog
+// actor's inputs (SCALARS) each tactical wave then writes the symlog
 // scalars and mission values of its 16 environments, one row per store (on
 // the scan waves they cost the scan kernel 6 µs and the plane kernel of the
-// next call 6 µs more; here they add about 5 µs to this kernel).
+// next call 6 µs more).
 //   * The workgroup first stages every input its chains read (all loads
 //     issued at once, coalesced over the rows' first 192 bytes), so the
 //     chains read LDS: read from global memory at their points of use, the
@@ -1328,7 +1351,7 @@ template <bool SCALARS>
 __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(OnboardRows rows) {
     __shared__ ControlStage stage;
     // Per controller wave: the workgroup's environments, BWB missions first.
-    __shared__ unsigned char order[4][64];
+    __shared__ unsigned char order[kControlWaves][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int a = lane & 3;
@@ -1402,37 +1425,40 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
         // environment e) into its own table and reads back its quads'
         // environments.  Every environment's values are the same in any
         // order.
-        int slot = lane;  // environment within the 64
-        if (w != 0) {
+        // Tactical waves: environment 16 (w - 4) + lane / 4.
+        int slot = 16 * (w - kControlWaves) + (lane >> 2);
+        if (w < kControlWaves) {
             const bool b = bwb_mission(stage.mission[lane]);
             const uint64_t bm = __builtin_amdgcn_ballot_w64(b);
             const unsigned nb = (unsigned)__builtin_popcountll(bm);
             const uint64_t mine = b ? bm : ~bm;
             const unsigned below = __builtin_amdgcn_mbcnt_hi(
                 (unsigned)(mine >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)mine, 0u));
-            order[w - 1][b ? below : nb + below] = (unsigned char)lane;
+            order[w][b ? below : nb + below] = (unsigned char)lane;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            slot = order[w - 1][16 * (w - 1) + (lane >> 2)];
+            slot = order[w][16 * w + (lane >> 2)];
         }
 
         const size_t env = base + (size_t)slot;
         if (env < rows.batch) {
             const float *obs = stage.obs[slot];
             const float *mission = stage.mission[slot];
-            if (w == 0) {
-                float t[24];
-                tactical_features(obs, mission, t);
-                float *tac = rows.tactical + env * 24;
+            if (w >= kControlWaves) {
+                // Lane a of the quad writes features 6a .. 6a + 5.
+                float t[6];
+                tactical_quad(obs, mission, a, t);
+                float *tac = rows.tactical + env * 24 + 6 * a;
 #pragma unroll
-                for (int i = 0; i < 24; ++i) tac[i] = t[i];
+                for (int i = 0; i < 6; ++i) tac[i] = t[i];
                 if (rows.proprio) {
-                    float *p = rows.proprio + env * 91, *mv = rows.mission_vec + env * 49;
+                    float *p = rows.proprio + env * 91 + 52 + 6 * a,
+                          *mv = rows.mission_vec + env * 49 + 10 + 6 * a;
 #pragma unroll
-                    for (int i = 0; i < 24; ++i) {
-                        p[52 + i] = t[i];
-                        mv[10 + i] = t[i];
+                    for (int i = 0; i < 6; ++i) {
+                        p[i] = t[i];
+                        mv[i] = t[i];
                     }
                 }
             } else {
@@ -1487,7 +1513,7 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
                 }
             }
         }
-        if (SCALARS && w > 0) {
+        if (SCALARS && w >= kControlWaves) {
             // Lane l's input: obs[l] (l < 48), obs[4144 + l - 48] (l < 52),
             // mission[l - 52] (l < 62).
             const int lo = min(lane, kStageObs - 1), lt = min(max(lane - 48, 0), 3),
@@ -1498,13 +1524,13 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
             float raw[16];
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const int e = 16 * (w - 1) + j;
+                const int e = 16 * (w - kControlWaves) + j;
                 raw[j] = lane < 48 ? stage.obs[e][lo]
                                    : (lane < 52 ? stage.tail[e][lt] : stage.mission[e][lm]);
             }
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const size_t env = base + (size_t)(16 * (w - 1) + j);
+                const size_t env = base + (size_t)(16 * (w - kControlWaves) + j);
                 const bool valid = env < rows.batch;
                 const size_t row = valid ? env : base;
                 actor_scalars(raw[j], lane, rows.proprio + row * 91, rows.mission_vec + row * 49,
