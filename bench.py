@@ -295,8 +295,10 @@ def _leg_onboard(torch, sets, steps, out, tac, pri):
                        _events_time(torch, onboard_call, steps, SUITE_WARMUP), BATCH,
                        onboard_bytes,
                        note="bytes_per_env: proprio, scan rays and mission read once, "
-                            "tactical and prior written once; latency- and issue-bound, "
-                            "not HBM-bound"))
+                            "tactical and prior written once, as if every mission used "
+                            "the full scan; environments whose mission uses no scan "
+                            "result read none of their rays, dodge missions rows 0-3 "
+                            "only; latency- and issue-bound, not HBM-bound"))
 
 
 def _leg_actor_prep(torch, sets, steps, out, tac, pri):

@@ -294,12 +294,54 @@ def test_without_diag_and_sizes(torch_cuda, hip):
         assert np.abs(tac - wt).max() <= TOL and np.abs(pri - wp).max() <= TOL
 
 
+# (m4, m5) pairs that select each use of the scan: none, the closest return
+# (dodge: m5 > 0.75), the corridor and cluster (slalom: m4 > 0.75 and
+# m5 <= 0.25), lateral (m4 > 0.75, m5 > 0.25: none), the flags' boundaries,
+# and non-finite values (mapped NaN -> 0, +-inf -> +-1 first).
+MISSION_CLASSES = [(0.0, 0.0), (0.0, 1.0), (1.0, 0.0), (1.0, 0.5), (0.75, 0.0),
+                   (0.0, 0.75), (0.0, np.nextafter(np.float32(0.75), np.float32(2))),
+                   (1.0, 0.25), (np.inf, np.nan), (np.nan, np.inf), (-np.inf, 1.2),
+                   (1.4, -1.4)]
+
+
+@pytest.mark.parametrize("variant", [0, 3, 5, 6])
+def test_scan_uses_by_mission(torch_cuda, hip, variant):
+    """The scan kernel computes only what an environment's mission uses of
+    the scan (nothing, the closest return, or the corridor and cluster),
+    unless the diagnostics row is asked for.  On 9,000 environments (so most
+    scan waves take three, with their needs mixed) cycling through the
+    mission classes above, the call without diagnostics must equal the call
+    with them bit for bit, and both the oracle."""
+    note(f"onboard scan uses by mission, variant {variant}, 9000 envs")
+    n = 9000
+    b = synth.make_batch(n, seed=900 + variant, variant=variant, threads=16)
+    obs = in_window(b.obs)
+    mission = b.mission.copy()
+    # SPECIAL's 3e38 inputs have a rule of their own (test_huge_finite_inputs)
+    obs[np.abs(obs) == np.float32(3e38)] = np.float32(7.5)
+    mission[np.abs(mission) == np.float32(3e38)] = np.float32(0.25)
+    cls = (np.arange(n) * 7 + np.arange(n) // 4096) % len(MISSION_CLASSES)
+    for c, (m4, m5) in enumerate(MISSION_CLASSES):
+        mission[cls == c, 4] = m4
+        mission[cls == c, 5] = m5
+    full = run_onboard(torch_cuda, hip, obs, mission, with_diag=True)
+    lazy = run_onboard(torch_cuda, hip, obs, mission, with_diag=False)
+    for g, w, name in zip(lazy[:2], full[:2], ("tactical", "prior")):
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), \
+            f"{name}: without diagnostics differs at envs {np.argwhere((g != w).any(1))[:5].ravel()}"
+    pick = np.random.default_rng(variant).choice(n, 1500, replace=False)
+    stats = compare(tuple(x[pick] for x in full), oracle.onboard(obs[pick], mission[pick]),
+                    f"variant{variant}")
+    note(f"scan uses variant {variant}: {stats}")
+
+
 def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
     """The scan grid has 4,096 waves; each forms the frames of its next 64
     environments at once, so a batch beyond 64 x 4,096 makes the first waves
     form a second group.  4,096 distinct environments are tiled on the device
     to 263,144 rows (4.4 GB of observations); every row must equal, bit for
-    bit, the same environment's row from the 4,096-row call."""
+    bit, the same environment's row from the 4,096-row call, with and without
+    the diagnostics row."""
     torch = torch_cuda
     distinct, batch = 4096, 64 * 4096 + 1000
     note(f"onboard {batch} envs tiled from {distinct} (second frame group)")
@@ -310,23 +352,29 @@ def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
     big_obs = obs.repeat(reps, 1)[:batch].contiguous()
     big_mis = mission.repeat(reps, 1)[:batch].contiguous()
 
-    def run(o, m):
+    def run(o, m, with_diag=True):
         n = o.shape[0]
         tac = torch.full((n, 24), float("nan"), dtype=torch.float32, device="cuda")
         pri = torch.full((n, 15), float("nan"), dtype=torch.float32, device="cuda")
-        diag = torch.full((n, oracle.ONBOARD_DIAG), float("nan"), dtype=torch.float32, device="cuda")
+        diag = torch.full((n, oracle.ONBOARD_DIAG), float("nan"), dtype=torch.float32,
+                          device="cuda") if with_diag else None
         s = torch.cuda.current_stream()
         assert hip.onboard_tactical_prior_device(o, m, tac, pri, diag, n, s) == 1
         assert hip.synchronize(s) == 1
-        return [t.cpu().numpy().view(np.uint32) for t in (tac, pri, diag)]
+        return [t.cpu().numpy().view(np.uint32) for t in (tac, pri) + ((diag,) if with_diag else ())]
 
     small = run(obs, mission)
     big = run(big_obs, big_mis)
+    # Without diagnostics the scan computes only what each mission uses.
+    big_lazy = run(big_obs, big_mis, with_diag=False)
     del big_obs, big_mis
     rows = np.arange(batch) % distinct
     for g, w, name in zip(big, small, ("tactical", "prior", "diag")):
         bad = np.argwhere((g != w[rows]).any(1)).ravel()
         assert not bad.size, f"{name} differs at rows {bad[:5]}"
+    for g, w, name in zip(big_lazy, small, ("tactical", "prior")):
+        bad = np.argwhere((g != w[rows]).any(1)).ravel()
+        assert not bad.size, f"{name} without diagnostics differs at rows {bad[:5]}"
 
 
 def test_argument_validation(hip):

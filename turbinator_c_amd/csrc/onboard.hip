@@ -22,7 +22,12 @@
 //     < settles it (the first in ray order); the cluster count comes from
 //     lane masks, and the cluster's y centres are added in float in ray
 //     order, as the reference does, because the sign of that sum picks the
-//     slalom lane;
+//     slalom lane.  The controller uses the closest return for dodge
+//     missions only and the corridor and cluster for slalom missions only
+//     (onboard_features.cuh:208-244), so unless the caller asks for the
+//     scan's diagnostics each environment gets only the part its mission
+//     uses, and the next environment's ranges are requested only as far as
+//     it needs them;
 //   * the tactical features and the controller (mission decode, targets,
 //     landing / standard / inversion / BWB laws, cannon) run in a second
 //     kernel from the parked scan results, both on one quad of lanes per
@@ -226,15 +231,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t obs_rsrc(const float *obs, boo
 // The 24 ranges lane l of an environment's wave owns: slot u = 2 row + half
 // is ray 128 row + 64 half + l (row = 6 head + el), so slots run in ray
 // order and each load instruction reads 256 contiguous LiDAR bytes.
-__device__ __forceinline__ void load_ranges(__amdgpu_buffer_rsrc_t obs, int lane,
+// Elevation rows 4..5 are read through `upper`, which a caller that needs
+// only the closest return (rows 0..3) gives 0 bytes: they then read zeros,
+// outside the scan window.
+__device__ __forceinline__ void load_ranges(__amdgpu_buffer_rsrc_t obs,
+                                            __amdgpu_buffer_rsrc_t upper, int lane,
                                             float (&rg)[kScanRays]) {
 #pragma unroll
     for (int u = 0; u < kScanRays; ++u) {
         const int row = u / 2, head = row / 6, el = row % 6;
         rg[u] = __builtin_bit_cast(
             float, __builtin_amdgcn_raw_buffer_load_b32(
-                       obs, 4 * (48 + lane), 4 * ((16 * head + el) * 128 + 64 * (u % 2)),
-                       kNontemporal));
+                       el < 4 ? obs : upper, 4 * (48 + lane),
+                       4 * ((16 * head + el) * 128 + 64 * (u % 2)), kNontemporal));
     }
 }
 
@@ -245,18 +254,19 @@ struct ScanFrame {
 };
 
 struct FrameObs {
-    float o1, o6, o7, o8, o9;
+    float o1, o6, o7, o8, o9, m4, m5;  // and the two mission values scan_need reads
 };
 
-__device__ __forceinline__ FrameObs load_frame_obs(const float *obs) {
-    return FrameObs{obs[1], obs[6], obs[7], obs[8], obs[9]};
+__device__ __forceinline__ FrameObs load_frame_obs(const float *obs, const float *mission) {
+    return FrameObs{obs[1], obs[6], obs[7], obs[8], obs[9], mission[4], mission[5]};
 }
 
-__device__ __forceinline__ ScanFrame scan_frame(FrameObs v) {
-    // An empty asm that takes the five values waits for their loads once,
+__device__ __forceinline__ ScanFrame scan_frame(FrameObs &v) {
+    // An empty asm that takes the seven values waits for their loads once,
     // here, instead of letting each load sink to its use inside the branchy
     // non-finite mapping (one memory round trip each).
-    asm volatile("" : "+v"(v.o1), "+v"(v.o6), "+v"(v.o7), "+v"(v.o8), "+v"(v.o9));
+    asm volatile("" : "+v"(v.o1), "+v"(v.o6), "+v"(v.o7), "+v"(v.o8), "+v"(v.o9), "+v"(v.m4),
+                 "+v"(v.m5));
     const Attitude att = attitude_of(ob_obs(v.o6), ob_obs(v.o7), ob_obs(v.o8), ob_obs(v.o9));
     ScanFrame f;
 #pragma unroll
@@ -330,6 +340,61 @@ __device__ __forceinline__ float add_in_lane_order(float sum, float v, uint64_t 
     return sum;
 }
 
+// The 618M actor's three LiDAR channel planes of the wave's 1,536 rays,
+// written into `planes`, the environment's [6][16][128] channel block: these
+// rays are in the wave's registers already, so the actor entry reads them
+// from HBM once, and its plane kernel writes only the other elevation rows.
+// Slot u holds row 6 head + el, azimuths 64 (u % 2) + lane: channel kind k
+// of head h is plane h + 2k, so each store writes 256 consecutive bytes of
+// one plane row.
+__device__ __forceinline__ void write_channel_planes(const float (&rg)[kScanRays],
+                                                     __amdgpu_buffer_rsrc_t planes, int lane) {
+#pragma unroll
+    for (int u = 0; u < kScanRays; ++u) {
+        const int row = u / 2, head = row / 6, el = row % 6;
+#pragma unroll
+        for (int kind = 0; kind < 3; ++kind)
+            __builtin_amdgcn_raw_buffer_store_b32(
+                __builtin_bit_cast(unsigned, lidar_channel(rg[u], kind)), planes, 4 * lane,
+                4 * ((head + 2 * kind) * 2048 + el * 128 + 64 * (u % 2)), kStorePolicy);
+    }
+}
+
+// What the controller uses of an environment's scan (onboard_features.cuh:
+// 107-109 for the mission flags, :208-244 for the uses): a dodge mission
+// uses the closest return (min_r and its world offset), a slalom mission the
+// corridor minimum and the cluster, and every other mission none of it.
+// The two flags exclude each other (dodge needs m5 > 0.75, slalom m5 <= 0.25).
+constexpr int kNeedNone = 0, kNeedClosest = 1, kNeedCorridor = 2, kNeedAll = 3;
+
+__device__ __forceinline__ int scan_need(float raw_m4, float raw_m5) {
+    const float m4 = ob_mission(raw_m4), m5 = ob_mission(raw_m5);
+    const bool lateral = m4 > 0.75f && m5 > 0.25f;
+    const bool slalom = m4 > 0.75f && !lateral;
+    const bool dodge = m5 > 0.75f;
+    return slalom ? kNeedCorridor : (dodge ? kNeedClosest : kNeedNone);
+}
+
+// Lane 0's closest-return fields of `out` from the winning ray and range
+// bits (onboard_features.cuh:202, the world offset in the reference's
+// operation order).
+__device__ __forceinline__ void closest_fields(int ray, unsigned min_bits, const RayPlanes &rays,
+                                               const ScanFrame &f, ScanResult &out) {
+    const float range = ray >= 0 ? __uint_as_float(min_bits) : 30.0f;
+    out.min_r = range;
+    out.min_r_dx = 0.0f;
+    out.min_r_dy = 0.0f;
+    out.min_ray = -1;
+    if (ray >= 0) {
+        const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
+        const float rwx = f.r[0] * dx + f.r[1] * dy + f.r[2] * dz;
+        const float rwy = f.r[3] * dx + f.r[4] * dy + f.r[5] * dz;
+        out.min_r_dx = rwx * range;
+        out.min_r_dy = rwy * range;
+        out.min_ray = ray;
+    }
+}
+
 // onboard_features.cuh:184-234 for one environment, on one wave (24 rays per
 // lane, no workgroup barrier).
 //   * The reference maps non-finite ranges to 0 / +-1000 first; both fail
@@ -354,31 +419,15 @@ __device__ __forceinline__ float add_in_lane_order(float sum, float v, uint64_t 
 //   * Once the ranges are consumed (listed, or swept by pass 1), the
 //     registers take the next environment's (`next`, a 0-byte resource when
 //     there is none): they have the rest of this environment to arrive.
-//   * `f` is wave-uniform.
-//   * With PLANES (the 618M actor's entry) the wave first writes the three
-//     LiDAR channel planes of its 1,536 rays into `planes`, the
-//     environment's [6][16][128] channel block: these rays are in its
-//     registers already, so the entry reads them from HBM once, and the
-//     plane kernel writes only the other elevation rows.
-template <bool PLANES>
+//   * `f` and `need` are wave-uniform.  With kNeedClosest only (a dodge
+//     mission) the listing covers elevation rows 0..3 and the corridor work
+//     is skipped; with kNeedCorridor only (slalom) the closest-return search
+//     is skipped; with kNeedNone nothing is listed.  The fields skipped keep
+//     their empty values.
 __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes &rays,
                                          const ScanFrame &f, __amdgpu_buffer_rsrc_t next,
-                                         __amdgpu_buffer_rsrc_t planes, int lane, u32x2 *list,
-                                         ScanResult &out) {
-    if (PLANES) {
-        // Slot u holds row 6 head + el, azimuths 64 (u % 2) + lane: channel
-        // kind k of head h is plane h + 2k, so each store writes 256
-        // consecutive bytes of one plane row.
-#pragma unroll
-        for (int u = 0; u < kScanRays; ++u) {
-            const int row = u / 2, head = row / 6, el = row % 6;
-#pragma unroll
-            for (int kind = 0; kind < 3; ++kind)
-                __builtin_amdgcn_raw_buffer_store_b32(
-                    __builtin_bit_cast(unsigned, lidar_channel(rg[u], kind)), planes, 4 * lane,
-                    4 * ((head + 2 * kind) * 2048 + el * 128 + 64 * (u % 2)), kStorePolicy);
-        }
-    }
+                                         __amdgpu_buffer_rsrc_t next_upper, int lane,
+                                         u32x2 *list, ScanResult &out, int need) {
     // List the in-window rays in slot order while counting them: entry =
     // (range bits - kWindowLo, ray).  The slot's first entry address is
     // uniform (scalar), so each lane's address is one shift-add of its lane
@@ -387,6 +436,10 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
     int n = 0;
 #pragma unroll
     for (int u = 0; u < kScanRays; ++u) {
+        // A mission that uses nothing lists nothing, and one that uses only
+        // the closest return lists elevation rows 0..3 only.
+        if (need == kNeedNone) break;
+        if (!(need & kNeedCorridor) && (u / 2) % 6 >= 4) continue;
         // A slot adds at most 64 entries, so the list can be full only from
         // slot kListCap / 64 + 1 on.
         if (64 * u > kListCap && n > kListCap) break;
@@ -420,7 +473,7 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        load_ranges(next, lane, rg);
+        load_ranges(next, next_upper, lane, rg);
         // Round r's values exist only when 64 r < n, and every later loop
         // stops at the same bound (initialising the unused rounds cost
         // about 35 moves per environment).
@@ -445,15 +498,17 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
                 key[r] = low_row ? off : kWindowSpan;
                 ray_of[r] = ray;
                 lane_min = min(lane_min, key[r]);
-                const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
-                const float rwx = f.r[0] * dx + f.r[1] * dy + f.r[2] * dz;
-                const float rwy = f.r[3] * dx + f.r[4] * dy + f.r[5] * dz;
-                const float rwz = f.r[6] * dx + f.r[7] * dy + f.r[8] * dz;
-                xl[r] = corridor_centre(rwx, rwy, rwz, range, f.py, yl[r]);
-                min_dx_c = fminf(min_dx_c, xl[r]);
+                if (need & kNeedCorridor) {
+                    const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
+                    const float rwx = f.r[0] * dx + f.r[1] * dy + f.r[2] * dz;
+                    const float rwy = f.r[3] * dx + f.r[4] * dy + f.r[5] * dz;
+                    const float rwz = f.r[6] * dx + f.r[7] * dy + f.r[8] * dz;
+                    xl[r] = corridor_centre(rwx, rwy, rwz, range, f.py, yl[r]);
+                    min_dx_c = fminf(min_dx_c, xl[r]);
+                }
             }
         }
-        const unsigned min_off = wave_min_u32(lane_min);
+        const unsigned min_off = (need & kNeedClosest) ? wave_min_u32(lane_min) : kWindowSpan;
         min_bits = min_off + kWindowLo;
         if (min_off != kWindowSpan) {
             // The list runs in ray order, so the first round and lane
@@ -468,27 +523,29 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
                 }
             }
         }
-        min_dx_c = wave_min(min_dx_c);
-        if (min_dx_c == 0.0f) {
-            // +0 and -0 tie; the reference keeps the first in ray order.
+        if (need & kNeedCorridor) {
+            min_dx_c = wave_min(min_dx_c);
+            if (min_dx_c == 0.0f) {
+                // +0 and -0 tie; the reference keeps the first in ray order.
+#pragma unroll
+                for (int r = 0; r < kListRounds; ++r) {
+                    if (64 * r >= n) break;
+                    const uint64_t zero = __builtin_amdgcn_ballot_w64(xl[r] == 0.0f);
+                    if (zero) {
+                        min_dx_c = __int_as_float(__builtin_amdgcn_readlane(
+                            __float_as_int(xl[r]), (int)__builtin_ctzll(zero)));
+                        break;
+                    }
+                }
+            }
+            const float limit = min_dx_c + 1.4f;
 #pragma unroll
             for (int r = 0; r < kListRounds; ++r) {
                 if (64 * r >= n) break;
-                const uint64_t zero = __builtin_amdgcn_ballot_w64(xl[r] == 0.0f);
-                if (zero) {
-                    min_dx_c = __int_as_float(__builtin_amdgcn_readlane(
-                        __float_as_int(xl[r]), (int)__builtin_ctzll(zero)));
-                    break;
-                }
+                const uint64_t members = __builtin_amdgcn_ballot_w64(xl[r] <= limit);
+                count += __builtin_popcountll(members);
+                y_sum = add_in_lane_order(y_sum, yl[r], members);
             }
-        }
-        const float limit = min_dx_c + 1.4f;
-#pragma unroll
-        for (int r = 0; r < kListRounds; ++r) {
-            if (64 * r >= n) break;
-            const uint64_t members = __builtin_amdgcn_ballot_w64(xl[r] <= limit);
-            count += __builtin_popcountll(members);
-            y_sum = add_in_lane_order(y_sum, yl[r], members);
         }
     } else {
         // Every slot.  The rays of rows el and el + 6 (heads 0 and 1) at the
@@ -543,7 +600,7 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        load_ranges(next, lane, rg);
+        load_ranges(next, next_upper, lane, rg);
         {
             // +0 and -0 tie; the reference keeps the first in ray order
             // (slot u holds rays 64 u .. 64 u + 63): the lowest ray among the
@@ -573,20 +630,7 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
         for (int u = 0; u < kScanRays; ++u) y_sum = add_in_lane_order(y_sum, yc[u], members[u]);
     }
     if (lane == 0) {
-        const int ray = min_ray;
-        const float range = min_ray >= 0 ? __uint_as_float(min_bits) : 30.0f;
-        out.min_r = range;
-        out.min_r_dx = 0.0f;
-        out.min_r_dy = 0.0f;
-        out.min_ray = -1;
-        if (ray >= 0) {
-            const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
-            const float rwx = f.r[0] * dx + f.r[1] * dy + f.r[2] * dz;
-            const float rwy = f.r[3] * dx + f.r[4] * dy + f.r[5] * dz;
-            out.min_r_dx = rwx * range;
-            out.min_r_dy = rwy * range;
-            out.min_ray = ray;
-        }
+        closest_fields(min_ray, min_bits, rays, f, out);
         out.min_dx_c = min_dx_c;
         out.cluster_count = count;
         out.cluster_y_sum = y_sum;
@@ -1241,10 +1285,11 @@ __device__ __forceinline__ void actor_scalars(float raw, int lane, float *propri
 // Phase 1: each wave scans one environment at a time; workgroups are
 // persistent (the ray table is loaded into LDS once per workgroup, the only
 // barrier).  Wave g of the grid takes environments g, g + W, g + 2W, ...
-// (W waves in the grid).  Their scan frames (attitude rows, py) are formed
-// up front, lane j for the wave's j-th environment, and each environment's
-// frame is then read from its lane into scalar registers.  Each
-// environment's ranges are requested while the previous one finishes.  The
+// (W waves in the grid).  Their scan frames (attitude rows, py) and scan
+// needs (scan_need) are formed up front, lane j for the wave's j-th
+// environment, and each environment's frame and need are then read from its
+// lane into scalar registers.  Each environment's ranges are requested while
+// the previous one finishes, as far as its need goes.  The
 // 32-byte result is parked in the environment's own prior row (60 bytes),
 // which phase 2 reads before it writes the 15 prior values there: no
 // scratch memory is needed.
@@ -1266,15 +1311,22 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
         return reinterpret_cast<const float *>(rows.obs + e * rows.obs_stride);
     };
     // Lane j forms the frame of the wave's j-th environment from here (a
-    // lane past the batch repeats the current one, whose row exists).
+    // lane past the batch repeats the current one, whose row exists), and
+    // what its mission uses of the scan (all of it when the caller asks for
+    // the scan's diagnostics).
     auto frame_obs = [&](size_t first) {
-        const size_t e = first + (size_t)lane * waves;
-        return load_frame_obs(obs_of(e < rows.batch ? e : first));
+        const size_t e0 = first + (size_t)lane * waves, e = e0 < rows.batch ? e0 : first;
+        return load_frame_obs(obs_of(e), reinterpret_cast<const float *>(
+                                             rows.mission + e * rows.mission_stride));
     };
-    const FrameObs first_obs = frame_obs(env);
+    auto frame_need = [&](const FrameObs &v) {
+        return rows.diag ? kNeedAll : scan_need(v.m4, v.m5);
+    };
+    FrameObs first_obs = frame_obs(env);
     float rg[kScanRays];
-    load_ranges(obs_rsrc(obs_of(env), true), lane, rg);
+    load_ranges(obs_rsrc(obs_of(env), true), obs_rsrc(obs_of(env), true), lane, rg);
     ScanFrame mine = scan_frame(first_obs);
+    int need_mine = frame_need(first_obs);
     for (int k = 0;;) {
         ScanFrame f;
 #pragma unroll
@@ -1285,12 +1337,25 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
                                   __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine.py), k));
         const size_t next_env = env + waves;
         const bool has_next = next_env < rows.batch;
+        // The next environment's ranges are requested only when it uses
+        // them (or when the actor's planes need them); the first
+        // environment of the next 64 has no need formed yet and is loaded.
+        const int need = __builtin_amdgcn_readlane(need_mine, k);
+        const int need_next = k + 1 < 64 ? __builtin_amdgcn_readlane(need_mine, (k + 1) & 63)
+                                         : kNeedAll;
+        const float *next_obs = has_next ? obs_of(next_env) : nullptr;
+        const __amdgpu_buffer_rsrc_t next =
+            obs_rsrc(next_obs, has_next && (PLANES || need_next != kNeedNone));
+        const __amdgpu_buffer_rsrc_t next_upper =
+            obs_rsrc(next_obs, has_next && (PLANES || (need_next & kNeedCorridor)));
+        if (PLANES)
+            write_channel_planes(
+                rg, __builtin_amdgcn_make_buffer_rsrc(rows.lidar + env * 12288, (short)0,
+                                                      12288 * 4, kBufferWord3),
+                lane);
         ScanResult s;
-        const __amdgpu_buffer_rsrc_t planes = __builtin_amdgcn_make_buffer_rsrc(
-            PLANES ? rows.lidar + env * 12288 : nullptr, (short)0, PLANES ? 12288 * 4 : 0,
-            kBufferWord3);
-        scan_env<PLANES>(rg, rays, f, obs_rsrc(has_next ? obs_of(next_env) : nullptr, has_next),
-                         planes, lane, lists[__builtin_amdgcn_readfirstlane(tid >> 6)], s);
+        scan_env(rg, rays, f, next, next_upper, lane, lists[__builtin_amdgcn_readfirstlane(tid >> 6)],
+                 s, need);
         if (lane == 0) {
             float *park = rows.prior + env * 15;
             park[0] = s.min_r;
@@ -1305,7 +1370,9 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
         env = next_env;
         if (++k == 64) {  // the next 64 environments of this wave
             k = 0;
-            mine = scan_frame(frame_obs(env));
+            FrameObs v = frame_obs(env);
+            mine = scan_frame(v);
+            need_mine = frame_need(v);
         }
     }
 }
