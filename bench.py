@@ -291,14 +291,16 @@ def _leg_onboard(torch, sets, steps, out, tac, pri):
     # H2 reads obs[0..47], the 1,536 scan rays (2 heads x 6 elevations x 128
     # azimuths) and the mission row, and writes 24 + 15 floats.
     onboard_bytes = 4 * (48 + 1536 + 10 + 24 + 15)
+    # No HBM rate is reported: the scan reads only the rays each mission uses
+    # (none for most missions, rows 0-3 for dodge), so the full-scan byte
+    # count would overstate the traffic.
     out.append(_report("onboard tactical+prior (16,384 envs)",
                        _events_time(torch, onboard_call, steps, SUITE_WARMUP), BATCH,
-                       onboard_bytes,
-                       note="bytes_per_env: proprio, scan rays and mission read once, "
-                            "tactical and prior written once, as if every mission used "
-                            "the full scan; environments whose mission uses no scan "
-                            "result read none of their rays, dodge missions rows 0-3 "
-                            "only; latency- and issue-bound, not HBM-bound"))
+                       None, full_scan_bytes_per_env=onboard_bytes,
+                       note="full_scan_bytes_per_env: proprio, scan rays and mission "
+                            "read once, tactical and prior written once, as if every "
+                            "mission used the full scan; latency- and issue-bound, "
+                            "not HBM-bound"))
 
 
 def _leg_actor_prep(torch, sets, steps, out, tac, pri):

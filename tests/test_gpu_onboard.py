@@ -335,16 +335,49 @@ def test_scan_uses_by_mission(torch_cuda, hip, variant):
     note(f"scan uses variant {variant}: {stats}")
 
 
+@pytest.mark.parametrize("n,classes", [(15, "mixed"), (16, "mixed"), (17, "mixed"),
+                                       (4097, "mixed"), (16384, "slalom"), (16384, "dodge")])
+def test_pooled_scan_sizes(torch_cuda, hip, n, classes):
+    """The H2 scan shares each workgroup's environments out from a pool in
+    LDS, one workgroup per CU with at least 16 environments each: batches
+    around one workgroup's share (15, 16, 17), one more than a full grid of
+    16 (4,097: the first workgroup takes 17), and full batches whose every
+    mission uses the corridor scan or the closest return (the pool holds
+    every environment).  Without diagnostics the call must equal the call
+    with them bit for bit, and both the oracle on a sample."""
+    note(f"onboard pooled scan, {n} envs, {classes} missions")
+    b = synth.make_batch(n, seed=1300 + n, variant=synth.ORDINARY, threads=16)
+    obs = in_window(b.obs)
+    mission = b.mission.copy()
+    if classes == "mixed":
+        cls = np.arange(n) % len(MISSION_CLASSES)
+        for c, (m4, m5) in enumerate(MISSION_CLASSES):
+            mission[cls == c, 4] = m4
+            mission[cls == c, 5] = m5
+    else:
+        mission[:, 4], mission[:, 5] = (1.0, 0.0) if classes == "slalom" else (0.0, 1.0)
+    full = run_onboard(torch_cuda, hip, obs, mission, with_diag=True)
+    lazy = run_onboard(torch_cuda, hip, obs, mission, with_diag=False)
+    for g, w, name in zip(lazy[:2], full[:2], ("tactical", "prior")):
+        assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), \
+            f"{name}: without diagnostics differs at envs {np.argwhere((g != w).any(1))[:5].ravel()}"
+    pick = np.random.default_rng(n).choice(n, min(n, 800), replace=False)
+    stats = compare(tuple(x[pick] for x in full), oracle.onboard(obs[pick], mission[pick]),
+                    f"pooled{n}{classes}")
+    note(f"pooled scan {n} {classes}: {stats}")
+
+
 def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
-    """The scan grid has 4,096 waves; each forms the frames of its next 64
-    environments at once, so a batch beyond 64 x 4,096 makes the first waves
-    form a second group.  4,096 distinct environments are tiled on the device
+    """The onboard entry's scan takes up to 1,024 environments per workgroup
+    and round (256 workgroups), so a batch beyond 262,144 makes every
+    workgroup take a second round.  4,096 distinct environments are tiled on
+    the device
     to 263,144 rows (4.4 GB of observations); every row must equal, bit for
     bit, the same environment's row from the 4,096-row call, with and without
     the diagnostics row."""
     torch = torch_cuda
     distinct, batch = 4096, 64 * 4096 + 1000
-    note(f"onboard {batch} envs tiled from {distinct} (second frame group)")
+    note(f"onboard {batch} envs tiled from {distinct} (second round)")
     b = synth.make_batch(distinct, seed=271, threads=16)
     obs = torch.from_numpy(in_window(b.obs)).cuda()
     mission = torch.from_numpy(b.mission).cuda()

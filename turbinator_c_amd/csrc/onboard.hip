@@ -27,7 +27,11 @@
 //     (onboard_features.cuh:208-244), so unless the caller asks for the
 //     scan's diagnostics each environment gets only the part its mission
 //     uses, and the next environment's ranges are requested only as far as
-//     it needs them;
+//     it needs them.  In the onboard entry the environments whose mission
+//     uses the scan are shared out over the 16 waves of a CU from a pool in
+//     LDS, so the waves that would have drawn several slalom missions do
+//     not set the kernel's time; the actor entry's scan, which also writes
+//     the LiDAR channels of every environment, keeps a static share;
 //   * the tactical features and the controller (mission decode, targets,
 //     landing / standard / inversion / BWB laws, cannon) run in a second
 //     kernel from the parked scan results, both on one quad of lanes per
@@ -1282,17 +1286,18 @@ __device__ __forceinline__ void actor_scalars(float raw, int lane, float *propri
         lane >= 52 && lane < 62 ? 4 * (lane - 52) : kPastRecords, 0, 0);
 }
 
-// Phase 1: each wave scans one environment at a time; workgroups are
-// persistent (the ray table is loaded into LDS once per workgroup, the only
-// barrier).  Wave g of the grid takes environments g, g + W, g + 2W, ...
-// (W waves in the grid).  Their scan frames (attitude rows, py) and scan
-// needs (scan_need) are formed up front, lane j for the wave's j-th
-// environment, and each environment's frame and need are then read from its
-// lane into scalar registers.  Each environment's ranges are requested while
-// the previous one finishes, as far as its need goes.  The
-// 32-byte result is parked in the environment's own prior row (60 bytes),
-// which phase 2 reads before it writes the 15 prior values there: no
-// scratch memory is needed.
+// Phase 1 of the actor entry.  Each wave scans one environment at a time;
+// workgroups are persistent (the ray table is loaded into LDS once per
+// workgroup, the only barrier).  Wave g of the grid takes environments g,
+// g + W, g + 2W, ... (W waves in the grid).  Their scan frames (attitude
+// rows, py) and scan needs (scan_need) are formed up front, lane j for the
+// wave's j-th environment, and each environment's frame and need are then
+// read from its lane into scalar registers.  Each environment's ranges are
+// requested while the previous one finishes, as far as its need goes (the
+// PLANES form reads every range: it writes the LiDAR channels of each
+// environment's scan rays).  The 32-byte result is parked in the
+// environment's own prior row (60 bytes), which phase 2 reads before it
+// writes the 15 prior values there: no scratch memory is needed.
 template <bool PLANES>
 __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows rows) {
     __shared__ RayPlanes rays;
@@ -1374,6 +1379,159 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
             mine = scan_frame(v);
             need_mine = frame_need(v);
         }
+    }
+}
+
+// Phase 1 of the H2 entry: the scan of the environments whose mission uses
+// it, shared out over a CU.  One workgroup of 16 waves per CU takes
+// environments g, g + G, g + 2G, ... (G workgroups in the grid), up to 1,024
+// per round.  Each wave forms the frames and needs of 64 of them (lane j the
+// j-th); an environment whose mission uses no scan result parks the empty
+// result from its lane, and the others are entered (frame, need) in the
+// workgroup's pool in LDS.  The waves then take pool entries one at a time
+// from a counter in LDS, the next one taken while the current one is
+// scanned so that its ranges are requested as far as its need goes.  Which
+// wave scans which environment varies from call to call; each result
+// depends only on its environment.  A static share of the environments
+// would leave the waves that drew several slalom missions working long after
+// the others: at 16,384 environments (four per wave) that wave sets the
+// kernel's time.
+constexpr int kPoolThreads = 1024;
+constexpr int kPoolWaves = kPoolThreads / 64;
+constexpr int kPoolRound = kPoolThreads;  // environments per round, one per thread
+constexpr unsigned kPoolBlocks = 256;     // one workgroup per CU
+struct PoolEntry {
+    unsigned env;  // kMaxBatch < 2^31
+    int need;
+    float r[9], py;
+};
+
+__device__ __forceinline__ void park_scan(float *park, const ScanResult &s) {
+    park[0] = s.min_r;
+    park[1] = s.min_r_dx;
+    park[2] = s.min_r_dy;
+    park[3] = s.min_dx_c;
+    park[4] = s.cluster_y_sum;
+    park[5] = __int_as_float(s.min_ray);
+    park[6] = __int_as_float(s.cluster_count);
+}
+
+__global__ __launch_bounds__(kPoolThreads) void onboard_scan_pool_kernel(OnboardRows rows) {
+    __shared__ RayPlanes rays;
+    __shared__ u32x2 lists[kPoolWaves][kListCap + 64];  // + a spare entry per lane
+    __shared__ PoolEntry pool[kPoolRound];
+    __shared__ int pool_count, pool_next;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    for (int i = tid; i < 1536; i += kPoolThreads) {
+        rays.d[0][i] = kRayDir[i * 3 + 0];
+        rays.d[1][i] = kRayDir[i * 3 + 1];
+        rays.d[2][i] = kRayDir[i * 3 + 2];
+    }
+    if (tid == 0) {
+        pool_count = 0;
+        pool_next = 0;
+    }
+    __syncthreads();
+    const size_t groups = gridDim.x;
+    // The launch gives every workgroup at least one environment.
+    const size_t mine = (rows.batch - blockIdx.x + groups - 1) / groups;
+    const size_t rounds = (mine + kPoolRound - 1) / kPoolRound;
+    auto obs_of = [&](size_t e) {
+        return reinterpret_cast<const float *>(rows.obs + e * rows.obs_stride);
+    };
+    // One lane takes the next entry for its wave.
+    auto take = [&]() {
+        int t = 0;
+        if (lane == 0)
+            t = __hip_atomic_fetch_add(&pool_next, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+        return __builtin_amdgcn_readfirstlane(t);
+    };
+    auto entry_env = [&](int t, size_t &env, int &need) {
+        env = (unsigned)__builtin_amdgcn_readfirstlane((int)pool[t].env);
+        need = __builtin_amdgcn_readfirstlane(pool[t].need);
+    };
+    auto entry_frame = [&](int t) {
+        ScanFrame f;
+#pragma unroll
+        for (int i = 0; i < 9; ++i)
+            f.r[i] = __builtin_bit_cast(
+                float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pool[t].r[i])));
+        f.py = __builtin_bit_cast(
+            float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, pool[t].py)));
+        return f;
+    };
+    u32x2 *list = lists[wave];
+    float rg[kScanRays];
+    for (size_t round = 0; round < rounds; ++round) {
+        // Thread x forms environment i = x of the round.
+        const size_t i = round * kPoolRound + (size_t)tid;
+        const size_t e = blockIdx.x + i * groups;
+        const bool valid = i < mine;
+        if (__builtin_amdgcn_readfirstlane((int)valid)) {  // lane 0 is valid whenever any lane is
+            const size_t row = valid ? e : blockIdx.x;
+            FrameObs v = load_frame_obs(
+                obs_of(row), reinterpret_cast<const float *>(rows.mission + row * rows.mission_stride));
+            const ScanFrame f = scan_frame(v);
+            const int need = rows.diag ? kNeedAll : scan_need(v.m4, v.m5);
+            const bool entered = valid && need != kNeedNone;
+            if (valid && !entered)
+                park_scan(rows.prior + e * 15, ScanResult{30.0f, 0.0f, 0.0f, 30.0f, 0.0f, -1, 0, 0});
+            const uint64_t m = __builtin_amdgcn_ballot_w64(entered);
+            int base = 0;
+            if (lane == 0 && m)
+                base = __hip_atomic_fetch_add(&pool_count, (int)__builtin_popcountll(m),
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            base = __builtin_amdgcn_readfirstlane(base);
+            if (entered) {
+                PoolEntry &p = pool[base + (int)__builtin_amdgcn_mbcnt_hi(
+                                               (unsigned)(m >> 32),
+                                               __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u))];
+                p.env = (unsigned)e;
+                p.need = need;
+#pragma unroll
+                for (int k = 0; k < 9; ++k) p.r[k] = f.r[k];
+                p.py = f.py;
+            }
+        }
+        __syncthreads();
+        const int count = __builtin_amdgcn_readfirstlane(pool_count);
+        int t = take();
+        if (t < count) {
+            size_t env;
+            int need;
+            entry_env(t, env, need);
+            load_ranges(obs_rsrc(obs_of(env), true),
+                        obs_rsrc(obs_of(env), (need & kNeedCorridor) != 0), lane, rg);
+            for (;;) {
+                const ScanFrame f = entry_frame(t);
+                // The next entry is taken before this one is scanned: the
+                // scan requests its ranges once these are consumed.
+                const int t_next = take();
+                const bool has_next = t_next < count;
+                size_t next_env = env;
+                int next_need = kNeedNone;
+                if (has_next) entry_env(t_next, next_env, next_need);
+                const float *next_obs = obs_of(next_env);
+                ScanResult s;
+                scan_env(rg, rays, f, obs_rsrc(next_obs, has_next),
+                         obs_rsrc(next_obs, has_next && (next_need & kNeedCorridor)), lane, list,
+                         s, need);
+                if (lane == 0) park_scan(rows.prior + env * 15, s);
+                if (!has_next) break;
+                t = t_next;
+                env = next_env;
+                need = next_need;
+            }
+        }
+        // Every wave has taken past the end of this round's pool.
+        __syncthreads();
+        if (tid == 0) {
+            pool_count = 0;
+            pool_next = 0;
+        }
+        __syncthreads();
     }
 }
 
@@ -1614,10 +1772,17 @@ int launch_onboard(const OnboardRows &rows, hipStream_t s) {
     const size_t scan_want = (rows.batch + kWavesPerBlock - 1) / kWavesPerBlock;
     const unsigned scan_blocks = scan_want > kScanBlocks ? kScanBlocks : (unsigned)scan_want;
     const size_t ctrl_want = (rows.batch + 63) / 64;
-    if (rows.lidar)
+    if (rows.lidar) {
         onboard_scan_kernel<true><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
-    else
+    } else if (!rows.proprio) {
+        // The H2 entry: the pooled scan, at least 16 environments per
+        // workgroup (one per wave) while that fills the chip.
+        const size_t want = (rows.batch + kPoolWaves - 1) / kPoolWaves;
+        onboard_scan_pool_kernel<<<want > kPoolBlocks ? kPoolBlocks : (unsigned)want,
+                                   kPoolThreads, 0, s>>>(rows);
+    } else {
         onboard_scan_kernel<false><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
+    }
     const unsigned ctrl_blocks = ctrl_want > kControlBlocks ? kControlBlocks : (unsigned)ctrl_want;
     if (rows.proprio)
         onboard_control_kernel<true><<<ctrl_blocks, kControlThreads, 0, s>>>(rows);
