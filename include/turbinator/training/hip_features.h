@@ -143,8 +143,12 @@ int tb_hip_lidar_transform_device(const float *ranges, float *out,
  * closest in-window return of elevations 0..3, its ray index
  * head*768 + el*128 + azi (-1 if none, as float), the corridor minimum, the
  * cluster count (as float) and the cluster's y sum, accumulated in float in
- * the reference's scan order (onboard_features.cuh:231-234).  Returns 0 for
- * NULL obs/mission/tactical/prior or batch 0 / above 0x7fffffff. */
+ * the reference's scan order (onboard_features.cuh:231-234).  Without
+ * `diag`, each environment's scan covers only what its mission uses (the
+ * closest return for dodge, the corridor and cluster for slalom, nothing
+ * otherwise), which is faster; tactical and prior are the same either way.
+ * Returns 0 for NULL obs/mission/tactical/prior or batch 0 / above
+ * 0x7fffffff. */
 int tb_hip_onboard_tactical_prior_device(const float *obs, const float *mission,
                                          float *tactical, float *prior, float *diag,
                                          size_t batch_size, void *stream);
