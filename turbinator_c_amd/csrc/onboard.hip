@@ -1400,6 +1400,12 @@ constexpr int kPoolThreads = 1024;
 constexpr int kPoolWaves = kPoolThreads / 64;
 constexpr int kPoolRound = kPoolThreads;  // environments per round, one per thread
 constexpr unsigned kPoolBlocks = 256;     // one workgroup per CU
+// The onboard entry's batch from which the pool pays.  Measured on one box
+// (static share -> pool, us): 2,048 envs 17.4 -> 17.9, 3,072 18.5 -> 18.1,
+// 4,096 19.6 -> 18.2, 16,384 28.4 -> 25.3; below 2,048 the pool is 0.9-1.5
+// us slower (the needs are formed before any range is requested, and a
+// workgroup holds at most a few environments whose mission uses the scan).
+constexpr size_t kPoolMinBatch = 2560;
 struct PoolEntry {
     unsigned env;  // kMaxBatch < 2^31
     int need;
@@ -1768,15 +1774,17 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
     }
 }
 
-int launch_onboard(const OnboardRows &rows, hipStream_t s) {
+// `pooled` selects the pooled scan, which holds a whole CU per workgroup:
+// for calls whose scan runs alone, not beside the actor's plane kernel.
+int launch_onboard(const OnboardRows &rows, hipStream_t s, bool pooled) {
     const size_t scan_want = (rows.batch + kWavesPerBlock - 1) / kWavesPerBlock;
     const unsigned scan_blocks = scan_want > kScanBlocks ? kScanBlocks : (unsigned)scan_want;
     const size_t ctrl_want = (rows.batch + 63) / 64;
     if (rows.lidar) {
         onboard_scan_kernel<true><<<scan_blocks, kBlockThreads, 0, s>>>(rows);
-    } else if (!rows.proprio) {
-        // The H2 entry: the pooled scan, at least 16 environments per
-        // workgroup (one per wave) while that fills the chip.
+    } else if (pooled) {
+        // At least 16 environments per workgroup (one per wave) while that
+        // fills the chip.
         const size_t want = (rows.batch + kPoolWaves - 1) / kPoolWaves;
         onboard_scan_pool_kernel<<<want > kPoolBlocks ? kPoolBlocks : (unsigned)want,
                                    kPoolThreads, 0, s>>>(rows);
@@ -1811,7 +1819,8 @@ extern "C" int tb_hip_onboard_tactical_prior_device(const float *obs, const floa
     rows.lidar = nullptr;
     rows.batch = batch_size;
     (void)hipGetLastError();
-    return launch_onboard(rows, reinterpret_cast<hipStream_t>(stream));
+    return launch_onboard(rows, reinterpret_cast<hipStream_t>(stream),
+                          batch_size >= kPoolMinBatch);
 }
 
 // ---------------------------------------------------------------------------
@@ -2057,8 +2066,8 @@ extern "C" int tb_hip_actor_inputs_device(const float *obs, const float *mission
     rows.mission_vec = mission_vec;
     rows.lidar = split ? lidar_channels : nullptr;
     rows.batch = batch_size;
-    if (!side) return launch_onboard(rows, s);
-    const int ok = launch_onboard(rows, side->stream);
+    if (!side) return launch_onboard(rows, s, false);
+    const int ok = launch_onboard(rows, side->stream, false);
     if (hipEventRecord(side->join, side->stream) != hipSuccess ||
         hipStreamWaitEvent(s, side->join, 0) != hipSuccess)
         return 0;
