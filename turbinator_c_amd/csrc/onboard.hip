@@ -408,13 +408,13 @@ __device__ __forceinline__ void closest_fields(int ray, unsigned min_bits, const
 //     `list` (ballot + lane prefix count) and passes 1 and 2 run over the
 //     list, 64 rays per instruction.  When more than kListCap rays are in
 //     the window, every slot is swept instead (the same per-ray arithmetic).
-//   * The closest return over elevation rows 0..3 is found in two steps: the
-//     wave's minimum in-window range (as bits: positive floats order like
-//     their bit patterns), then the first slot in ray order and the first
-//     lane holding exactly that range, from lane masks on the scalar unit.
-//     That is the reference's first minimum in scan order.  Lane 0
-//     recomputes the winner's world offset with the reference's expression,
-//     which gives the value pass 1 formed (see the pair identity below).
+//   * The closest return over elevation rows 0..3 is found straight from
+//     the ranges, before any list, in two steps: the wave's minimum
+//     in-window range (as bits: positive floats order like their bit
+//     patterns), then the first slot in ray order and the first lane holding
+//     exactly that range, from lane masks on the scalar unit.  That is the
+//     reference's first minimum in scan order.  Lane 0 computes the winner's
+//     world offset with the reference's expression.
 //   * Pass 1 keeps each ray's corridor centre (x = +inf outside the window or
 //     the corridor), so pass 2 is a compare-and-add.  The reference's
 //     strict-< update over corridor rays is the minimum of their centres,
@@ -423,15 +423,45 @@ __device__ __forceinline__ void closest_fields(int ray, unsigned min_bits, const
 //   * Once the ranges are consumed (listed, or swept by pass 1), the
 //     registers take the next environment's (`next`, a 0-byte resource when
 //     there is none): they have the rest of this environment to arrive.
-//   * `f` and `need` are wave-uniform.  With kNeedClosest only (a dodge
-//     mission) the listing covers elevation rows 0..3 and the corridor work
-//     is skipped; with kNeedCorridor only (slalom) the closest-return search
-//     is skipped; with kNeedNone nothing is listed.  The fields skipped keep
-//     their empty values.
+//   * `f` and `need` are wave-uniform.  Only the corridor and cluster use
+//     the list: with kNeedClosest only (a dodge mission) nothing is listed
+//     and the corridor work is skipped; with kNeedCorridor only (slalom) the
+//     closest-return search is skipped; with kNeedNone nothing is done.  The
+//     fields skipped keep their empty values.
 __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes &rays,
                                          const ScanFrame &f, __amdgpu_buffer_rsrc_t next,
                                          __amdgpu_buffer_rsrc_t next_upper, int lane,
                                          u32x2 *list, ScanResult &out, int need) {
+    // Closest return, straight from the ranges: each lane's minimum over its
+    // 16 slots of elevation rows 0..3 as bits (positive floats order like
+    // their bits; a ray outside the window counts as 11.5, the window's
+    // exclusive upper bound, so it never wins), the wave's minimum, then the
+    // first slot (slots are in ray order) and its first lane holding exactly
+    // that range: the reference's first minimum in scan order.
+    constexpr unsigned kWindowTop = 0x41380000u;  // 11.5f
+    unsigned min_bits = kWindowTop;
+    int min_ray = -1;
+    if (need & kNeedClosest) {
+        unsigned lane_min = kWindowTop;
+#pragma unroll
+        for (int u = 0; u < kScanRays; ++u) {
+            if ((u / 2) % 6 >= 4) continue;
+            lane_min = min(lane_min, rg[u] > 0.35f ? __float_as_uint(rg[u]) : kWindowTop);
+        }
+        min_bits = wave_min_u32(lane_min);
+        if (min_bits != kWindowTop) {
+            // Visiting slots from the last to the first leaves the first slot
+            // (in ray order) that holds the range, at its first lane.
+#pragma unroll
+            for (int u = kScanRays - 1; u >= 0; --u) {
+                if ((u / 2) % 6 >= 4) continue;
+                const uint64_t hit =
+                    __builtin_amdgcn_ballot_w64(__float_as_uint(rg[u]) == min_bits);
+                if (hit) min_ray = 64 * u + (int)__builtin_ctzll(hit);
+            }
+        }
+    }
+
     // List the in-window rays in slot order while counting them: entry =
     // (range bits - kWindowLo, ray).  The slot's first entry address is
     // uniform (scalar), so each lane's address is one shift-add of its lane
@@ -440,10 +470,8 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
     int n = 0;
 #pragma unroll
     for (int u = 0; u < kScanRays; ++u) {
-        // A mission that uses nothing lists nothing, and one that uses only
-        // the closest return lists elevation rows 0..3 only.
-        if (need == kNeedNone) break;
-        if (!(need & kNeedCorridor) && (u / 2) % 6 >= 4) continue;
+        // Only the corridor and cluster use the list.
+        if (!(need & kNeedCorridor)) break;
         // A slot adds at most 64 entries, so the list can be full only from
         // slot kListCap / 64 + 1 on.
         if (64 * u > kListCap && n > kListCap) break;
@@ -464,11 +492,6 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
         n += (int)__builtin_popcountll(m);
     }
 
-    // Closest return: a ray outside the window or on elevation rows 4..5
-    // counts as 11.5, the window's exclusive upper bound, so it never wins.
-    constexpr unsigned kWindowTop = 0x41380000u;  // 11.5f
-    unsigned min_bits;
-    int min_ray = -1;
     float min_dx_c = 30.0f;
     int count = 0;
     float y_sum = 0.0f;
@@ -482,9 +505,6 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
         // stops at the same bound (initialising the unused rounds cost
         // about 35 moves per environment).
         float xl[kListRounds], yl[kListRounds];
-        unsigned key[kListRounds];
-        int ray_of[kListRounds];
-        unsigned lane_min = kWindowSpan;
 #pragma unroll
         for (int r = 0; r < kListRounds; ++r) {
             if (64 * r < n) {
@@ -496,35 +516,12 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
                 const unsigned off = valid ? entry.x : kWindowSpan;
                 const float range = __uint_as_float(off + kWindowLo);
                 const int ray = valid ? (int)entry.y : 0;
-                // Ray 128 row + azimuth, row = 6 head + el: el < 4 on rows
-                // 0..3 and 6..9.
-                const bool low_row = ((0x3cfu >> (ray >> 7)) & 1u) != 0u;
-                key[r] = low_row ? off : kWindowSpan;
-                ray_of[r] = ray;
-                lane_min = min(lane_min, key[r]);
-                if (need & kNeedCorridor) {
-                    const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
-                    const float rwx = f.r[0] * dx + f.r[1] * dy + f.r[2] * dz;
-                    const float rwy = f.r[3] * dx + f.r[4] * dy + f.r[5] * dz;
-                    const float rwz = f.r[6] * dx + f.r[7] * dy + f.r[8] * dz;
-                    xl[r] = corridor_centre(rwx, rwy, rwz, range, f.py, yl[r]);
-                    min_dx_c = fminf(min_dx_c, xl[r]);
-                }
-            }
-        }
-        const unsigned min_off = (need & kNeedClosest) ? wave_min_u32(lane_min) : kWindowSpan;
-        min_bits = min_off + kWindowLo;
-        if (min_off != kWindowSpan) {
-            // The list runs in ray order, so the first round and lane
-            // holding the minimum is the reference's first minimum.
-#pragma unroll
-            for (int r = 0; r < kListRounds; ++r) {
-                if (64 * r >= n) break;
-                const uint64_t hit = __builtin_amdgcn_ballot_w64(key[r] == min_off);
-                if (hit) {
-                    min_ray = __builtin_amdgcn_readlane(ray_of[r], (int)__builtin_ctzll(hit));
-                    break;
-                }
+                const float dx = rays.d[0][ray], dy = rays.d[1][ray], dz = rays.d[2][ray];
+                const float rwx = f.r[0] * dx + f.r[1] * dy + f.r[2] * dz;
+                const float rwy = f.r[3] * dx + f.r[4] * dy + f.r[5] * dz;
+                const float rwz = f.r[6] * dx + f.r[7] * dy + f.r[8] * dz;
+                xl[r] = corridor_centre(rwx, rwy, rwz, range, f.py, yl[r]);
+                min_dx_c = fminf(min_dx_c, xl[r]);
             }
         }
         if (need & kNeedCorridor) {
@@ -558,24 +555,6 @@ __device__ __forceinline__ void scan_env(float (&rg)[kScanRays], const RayPlanes
         // head-1 sum is therefore P - Q where the head-0 sum is P + Q,
         // exactly (a + (-b) and a - b are the same IEEE operation), so each
         // pair reads one direction and forms P and Q once.
-        unsigned lane_min = kWindowTop;
-#pragma unroll
-        for (int u = 0; u < kScanRays; ++u) {
-            if ((u / 2) % 6 >= 4) continue;
-            lane_min = min(lane_min, rg[u] > 0.35f ? __float_as_uint(rg[u]) : kWindowTop);
-        }
-        min_bits = wave_min_u32(lane_min);
-        if (min_bits != kWindowTop) {
-            // Visiting slots from the last to the first leaves the first slot
-            // (in ray order) that holds the range, at its first lane.
-#pragma unroll
-            for (int u = kScanRays - 1; u >= 0; --u) {
-                if ((u / 2) % 6 >= 4) continue;
-                const uint64_t hit =
-                    __builtin_amdgcn_ballot_w64(__float_as_uint(rg[u]) == min_bits);
-                if (hit) min_ray = 64 * u + (int)__builtin_ctzll(hit);
-            }
-        }
         float xc[kScanRays], yc[kScanRays];
         int min_slot = kScanRays;
 #pragma unroll
@@ -1429,6 +1408,13 @@ __global__ __launch_bounds__(kPoolThreads) void onboard_scan_pool_kernel(Onboard
     __shared__ int pool_count, pool_next;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const size_t groups = gridDim.x;
+    // The launch gives every workgroup at least one environment.
+    const size_t mine = (rows.batch - blockIdx.x + groups - 1) / groups;
+    const size_t rounds = (mine + kPoolRound - 1) / kPoolRound;
+    auto obs_of = [&](size_t e) {
+        return reinterpret_cast<const float *>(rows.obs + e * rows.obs_stride);
+    };
     for (int i = tid; i < 1536; i += kPoolThreads) {
         rays.d[0][i] = kRayDir[i * 3 + 0];
         rays.d[1][i] = kRayDir[i * 3 + 1];
@@ -1439,13 +1425,6 @@ __global__ __launch_bounds__(kPoolThreads) void onboard_scan_pool_kernel(Onboard
         pool_next = 0;
     }
     __syncthreads();
-    const size_t groups = gridDim.x;
-    // The launch gives every workgroup at least one environment.
-    const size_t mine = (rows.batch - blockIdx.x + groups - 1) / groups;
-    const size_t rounds = (mine + kPoolRound - 1) / kPoolRound;
-    auto obs_of = [&](size_t e) {
-        return reinterpret_cast<const float *>(rows.obs + e * rows.obs_stride);
-    };
     // One lane takes the next entry for its wave.
     auto take = [&]() {
         int t = 0;
