@@ -288,19 +288,29 @@ def _leg_onboard(torch, sets, steps, out, tac, pri):
     def onboard_call(i, s):
         o, m, _, _ = sets[i % len(sets)]
         assert features.onboard_tactical_prior_device(o, m, tac, pri, None, BATCH, s) == 1
-    # H2 reads obs[0..47], the 1,536 scan rays (2 heads x 6 elevations x 128
-    # azimuths) and the mission row, and writes 24 + 15 floats.
-    onboard_bytes = 4 * (48 + 1536 + 10 + 24 + 15)
-    # No HBM rate is reported: the scan reads only the rays each mission uses
-    # (none for most missions, rows 0-3 for dodge), so the full-scan byte
-    # count would overstate the traffic.
+    # H2 reads obs[0..47] and the mission row and writes 24 + 15 floats for
+    # every environment; of the 1,536 scan rays (2 heads x 6 elevations x 128
+    # azimuths) it reads those the mission uses: rows 0-3 (1,024 rays) for a
+    # dodge mission (m5 > 0.75), all of them for a slalom mission (m4 > 0.75,
+    # m5 <= 0.25), none otherwise (onboard_features.cuh:208-244).
+    fixed = 4 * (48 + 10 + 24 + 15)
+    full_scan = fixed + 4 * 1536
+    ray_bytes = []
+    for _, m, _, _ in sets:
+        mis = np.nan_to_num(m[:, 4:6].cpu().numpy(), nan=0.0, posinf=1.0, neginf=-1.0)
+        m4, m5 = mis[:, 0], mis[:, 1]
+        slalom = (m4 > 0.75) & (m5 <= 0.25)
+        dodge = m5 > 0.75
+        ray_bytes.append(float(np.where(slalom, 4 * 1536, np.where(dodge, 4 * 1024, 0)).mean()))
+    onboard_bytes = int(round(fixed + sum(ray_bytes) / len(ray_bytes)))
     out.append(_report("onboard tactical+prior (16,384 envs)",
                        _events_time(torch, onboard_call, steps, SUITE_WARMUP), BATCH,
-                       None, full_scan_bytes_per_env=onboard_bytes,
-                       note="full_scan_bytes_per_env: proprio, scan rays and mission "
-                            "read once, tactical and prior written once, as if every "
-                            "mission used the full scan; latency- and issue-bound, "
-                            "not HBM-bound"))
+                       onboard_bytes, full_scan_bytes_per_env=full_scan,
+                       note="bytes_per_env: proprio and mission read once, tactical and "
+                            "prior written once, and the scan rays each environment's "
+                            "mission uses (rows 0-3 for dodge, all for slalom, none "
+                            "otherwise; this batch's average); full_scan_bytes_per_env "
+                            "counts every scan ray; latency-bound, not HBM-bound"))
 
 
 def _leg_actor_prep(torch, sets, steps, out, tac, pri):
