@@ -336,16 +336,20 @@ def test_scan_uses_by_mission(torch_cuda, hip, variant):
 
 
 @pytest.mark.parametrize("n,classes", [(2560, "mixed"), (2561, "mixed"), (4097, "mixed"),
-                                       (16384, "slalom"), (16384, "dodge")])
+                                       (10240, "mixed"), (16384, "slalom"), (16384, "dodge"),
+                                       (16385, "mixed")])
 def test_pooled_scan_sizes(torch_cuda, hip, n, classes):
-    """From 2,560 environments the H2 scan shares each workgroup's
-    environments out from a pool in LDS, with at least 16 environments per
-    workgroup and at most 256 workgroups: the smallest pooled batch (160
-    workgroups of 16), one more (161 workgroups, 15 or 16 each), one more
-    than a full grid of 16 (4,097: the first workgroup takes 17), and full
-    batches whose every mission uses the corridor scan or the closest return
-    (the pool holds every environment).  Without diagnostics the call must
-    equal the call with them bit for bit, and both the oracle on a sample."""
+    """The H2 entry's scan forms by batch: from 2,560 environments the scan
+    kernel shares each workgroup's environments out from a pool in LDS, with
+    at least 16 per workgroup and at most 256 workgroups: the smallest pooled
+    batch (160 workgroups of 16), one more (161 workgroups, 15 or 16 each)
+    and one more than a full grid of 16 (4,097: the first workgroup takes
+    17).  From 10,240 to 16,384 environments one kernel scans and controls
+    each workgroup's 64 environments: its smallest batch, and full batches
+    whose every mission uses the corridor scan or the closest return (the
+    pool holds every environment).  16,385 goes back to two kernels.
+    Without diagnostics the call must equal the call with them bit for bit,
+    and both the oracle on a sample."""
     note(f"onboard pooled scan, {n} envs, {classes} missions")
     b = synth.make_batch(n, seed=1300 + n, variant=synth.ORDINARY, threads=16)
     obs = in_window(b.obs)
@@ -368,16 +372,17 @@ def test_pooled_scan_sizes(torch_cuda, hip, n, classes):
     note(f"pooled scan {n} {classes}: {stats}")
 
 
-def test_scan_forms_agree(torch_cuda, hip):
-    """Below 2,560 environments the H2 entry scans with a static share of the
-    environments per wave, from 2,560 with the pool.  The same 2,560
-    environments (missions cycling through every class) called as 2,559 and
-    as 2,560 must give the same first 2,559 rows bit for bit, with and
-    without diagnostics."""
+@pytest.mark.parametrize("n", [2560, 10240, 16385])
+def test_scan_forms_agree(torch_cuda, hip, n):
+    """The H2 entry changes form at these batches: a static share of the
+    environments per scan wave below 2,560, the pooled scan kernel from
+    there, one kernel for scan and control from 10,240 to 16,384, and the
+    pooled scan kernel again above.  The same n environments (missions
+    cycling through every class) called as n - 1 and as n must give the same
+    first n - 1 rows bit for bit, with and without diagnostics."""
     torch = torch_cuda
-    n = 2560
-    note(f"onboard static vs pooled scan, {n - 1} / {n} envs")
-    b = synth.make_batch(n, seed=2560, variant=synth.ORDINARY, threads=16)
+    note(f"onboard scan forms at {n - 1} / {n} envs")
+    b = synth.make_batch(n, seed=n, variant=synth.ORDINARY, threads=16)
     obs = in_window(b.obs)
     mission = b.mission.copy()
     cls = np.arange(n) % len(MISSION_CLASSES)
@@ -385,9 +390,9 @@ def test_scan_forms_agree(torch_cuda, hip):
         mission[cls == c, 4] = m4
         mission[cls == c, 5] = m5
     for with_diag in (True, False):
-        pooled = run_onboard(torch, hip, obs, mission, with_diag=with_diag)
-        static = run_onboard(torch, hip, obs[:n - 1], mission[:n - 1], with_diag=with_diag)
-        for g, w, name in zip(static, pooled, ("tactical", "prior", "diag")):
+        larger = run_onboard(torch, hip, obs, mission, with_diag=with_diag)
+        smaller = run_onboard(torch, hip, obs[:n - 1], mission[:n - 1], with_diag=with_diag)
+        for g, w, name in zip(smaller, larger, ("tactical", "prior", "diag")):
             if g is None:
                 continue
             assert np.array_equal(g.view(np.uint32), w[:n - 1].view(np.uint32)), \

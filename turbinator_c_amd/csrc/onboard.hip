@@ -37,7 +37,12 @@
 //     kernel from the parked scan results, both on one quad of lanes per
 //     environment (lane a evaluates arm a and a quarter of the independent
 //     transcendental calls).  The controller's long register-heavy chain is
-//     kept apart from the scan so both keep their occupancy.  The angles
+//     kept apart from the scan so both keep their occupancy, except where
+//     the batch is one round of 64-environment workgroups over most CUs
+//     (the onboard entry from 10,240 to 16,384 environments): there one
+//     kernel does both, each workgroup scanning its own environments into
+//     LDS before their controller runs, which saves the second launch and
+//     the parked results' round trip.  The angles
 //     that reach its angle wraps use a correctly rounded atan2: exact angles
 //     (from equal or zero components) reach a wrap's discontinuity, where
 //     one ulp flips the wrapped error's sign.
@@ -55,6 +60,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "turbinator/training/hip_features.h"
 #include "recip_range.h"
@@ -1385,6 +1391,16 @@ constexpr unsigned kPoolBlocks = 256;     // one workgroup per CU
 // us slower (the needs are formed before any range is requested, and a
 // workgroup holds at most a few environments whose mission uses the scan).
 constexpr size_t kPoolMinBatch = 2560;
+// The onboard entry's batches that take the one-kernel form (each
+// workgroup scans its own 64 environments, then runs their controller):
+// those that fill at least 160 of the 256 CUs with one round of 64-
+// environment workgroups.  Measured on one box (two kernels -> one, us):
+// 8,192 envs 20.6 -> 21.4, 10,240 21.95 -> 21.65, 12,288 23.3 -> 21.8,
+// 14,336 24.4 -> 22.1, 16,384 25.4 -> 22.4; with a second round it loses
+// (18,432 36.3 -> 38.8, 65,536 79.4 -> 82.2), as it does with fewer
+// workgroups than CUs (4,096 18.3 -> 21.1): the two-kernel form spreads the
+// scan over every CU.
+constexpr size_t kFusedMinBatch = 160 * 64, kFusedMaxBatch = 256 * 64;
 struct PoolEntry {
     unsigned env;  // kMaxBatch < 2^31
     int need;
@@ -1557,71 +1573,186 @@ __device__ __forceinline__ bool bwb_mission(const float *raw) {
            (m6 > 0.75f && m5 > 0.60f);
 }
 
-template <bool SCALARS>
+// FUSED: the workgroup also scans its own environments (the onboard
+// entry's one-kernel form), from a pool in LDS over its eight waves, and the
+// results go straight into the stage.
+struct FusedScanLds {
+    RayPlanes rays;
+    u32x2 lists[2 * kControlWaves][kListCap + 64];  // + a spare entry per lane
+    PoolEntry pool[64];
+    int count, next;
+};
+
+// The scan of the workgroup's 64 staged environments (base + e), called by
+// every wave after the stage is written: wave 0 forms each environment's
+// frame and need from the stage (lane e), writes the empty result of those
+// whose mission uses no scan result and enters the others in the pool; then
+// every wave takes entries one at a time, the next one taken before the
+// current one is scanned so that its ranges are requested as far as its
+// need goes, and lane 0 writes each result into the stage.  Ends with the
+// workgroup's barrier, so the results are visible to the control phase.
+__device__ __forceinline__ void fused_scan(const OnboardRows &rows, size_t base,
+                                           ControlStage &stage, FusedScanLds &fused, int w,
+                                           int lane) {
+    auto obs_of = [&](size_t e) {
+        return reinterpret_cast<const float *>(rows.obs + e * rows.obs_stride);
+    };
+    auto stage_result = [&](int e, const ScanResult &r) {
+        float *sc = stage.scan[e];
+        sc[0] = r.min_r;
+        sc[1] = r.min_r_dx;
+        sc[2] = r.min_r_dy;
+        sc[3] = r.min_dx_c;
+        sc[4] = r.cluster_y_sum;
+        sc[5] = __int_as_float(r.min_ray);
+        sc[6] = __int_as_float(r.cluster_count);
+    };
+    if (w == 0) {
+        const int e = lane;
+        const bool valid = base + (size_t)e < rows.batch;
+        FrameObs v{stage.obs[e][1], stage.obs[e][6], stage.obs[e][7], stage.obs[e][8],
+                   stage.obs[e][9], stage.mission[e][4], stage.mission[e][5]};
+        const ScanFrame f = scan_frame(v);
+        const int need = rows.diag ? kNeedAll : scan_need(v.m4, v.m5);
+        const bool entered = valid && need != kNeedNone;
+        if (valid && !entered) stage_result(e, ScanResult{30.0f, 0.0f, 0.0f, 30.0f, 0.0f, -1, 0, 0});
+        const uint64_t m = __builtin_amdgcn_ballot_w64(entered);
+        if (entered) {
+            PoolEntry &p = fused.pool[__builtin_amdgcn_mbcnt_hi(
+                (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u))];
+            p.env = (unsigned)e;
+            p.need = need;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) p.r[k] = f.r[k];
+            p.py = f.py;
+        }
+        if (lane == 0) {
+            fused.count = (int)__builtin_popcountll(m);
+            fused.next = 0;
+        }
+    }
+    __syncthreads();
+    const int count = __builtin_amdgcn_readfirstlane(fused.count);
+    auto take = [&]() {
+        int t = 0;
+        if (lane == 0)
+            t = __hip_atomic_fetch_add(&fused.next, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_WORKGROUP);
+        return __builtin_amdgcn_readfirstlane(t);
+    };
+    auto entry = [&](int t, int &slot, int &need) {
+        slot = __builtin_amdgcn_readfirstlane((int)fused.pool[t].env);
+        need = __builtin_amdgcn_readfirstlane(fused.pool[t].need);
+    };
+    int t = take();
+    if (t < count) {
+        int slot, need;
+        entry(t, slot, need);
+        float rg[kScanRays];
+        const float *o = obs_of(base + (size_t)slot);
+        load_ranges(obs_rsrc(o, true), obs_rsrc(o, (need & kNeedCorridor) != 0), lane, rg);
+        for (;;) {
+            ScanFrame f;
+#pragma unroll
+            for (int i = 0; i < 9; ++i)
+                f.r[i] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fused.pool[t].r[i])));
+            f.py = __builtin_bit_cast(
+                float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, fused.pool[t].py)));
+            const int t_next = take();
+            const bool has_next = t_next < count;
+            int next_slot = slot, next_need = kNeedNone;
+            if (has_next) entry(t_next, next_slot, next_need);
+            const float *next_obs = obs_of(base + (size_t)next_slot);
+            ScanResult r;
+            scan_env(rg, fused.rays, f, obs_rsrc(next_obs, has_next),
+                     obs_rsrc(next_obs, has_next && (next_need & kNeedCorridor)), lane,
+                     fused.lists[w], r, need);
+            if (lane == 0) stage_result(slot, r);
+            if (!has_next) break;
+            t = t_next;
+            slot = next_slot;
+            need = next_need;
+        }
+    }
+    __syncthreads();
+}
+
+template <bool SCALARS, bool FUSED>
 __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(OnboardRows rows) {
+    constexpr int CW = kControlWaves, N = 64, kThreads = kControlThreads;
     __shared__ ControlStage stage;
     // Per controller wave: the workgroup's environments, BWB missions first.
-    __shared__ unsigned char order[kControlWaves][64];
+    __shared__ unsigned char order[CW][N];
+    __shared__ std::conditional_t<FUSED, FusedScanLds, char> fused;
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int a = lane & 3;
-    for (size_t base = (size_t)blockIdx.x * 64; base < rows.batch;
-         base += (size_t)gridDim.x * 64) {
+    if constexpr (FUSED) {
+        for (int i = tid; i < 1536; i += kThreads) {
+            fused.rays.d[0][i] = kRayDir[i * 3 + 0];
+            fused.rays.d[1][i] = kRayDir[i * 3 + 1];
+            fused.rays.d[2][i] = kRayDir[i * 3 + 2];
+        }
+    }
+    for (size_t base = (size_t)blockIdx.x * N; base < rows.batch;
+         base += (size_t)gridDim.x * N) {
         // Rows past the batch end re-read the last row; nothing uses them.
         auto row_of = [&](int e) {
             const size_t env = base + (size_t)e;
             return env < rows.batch ? env : rows.batch - 1;
         };
-        constexpr int kObsLoads = (64 * kStageObs + kControlThreads - 1) / kControlThreads;
-        constexpr int kMissionLoads = (64 * 10 + kControlThreads - 1) / kControlThreads;
-        constexpr int kScanLoads = (64 * 7 + kControlThreads - 1) / kControlThreads;
+        constexpr int kObsLoads = (N * kStageObs + kThreads - 1) / kThreads;
+        constexpr int kMissionLoads = (N * 10 + kThreads - 1) / kThreads;
+        constexpr int kScanLoads = (N * 7 + kThreads - 1) / kThreads;
         // Every thread issues all its loads unconditionally (an index past
         // the stage re-reads the stage's last value), so they leave at once.
         float vo[kObsLoads], vm[kMissionLoads], vs[kScanLoads], vt = 0.0f;
 #pragma unroll
         for (int k = 0; k < kObsLoads; ++k) {
-            const int idx = min(tid + kControlThreads * k, 64 * kStageObs - 1);
+            const int idx = min(tid + kThreads * k, N * kStageObs - 1);
             const int e = idx / kStageObs, i = idx - kStageObs * e;
             vo[k] = reinterpret_cast<const float *>(rows.obs + row_of(e) * rows.obs_stride)[i];
         }
 #pragma unroll
         for (int k = 0; k < kMissionLoads; ++k) {
-            const int idx = min(tid + kControlThreads * k, 64 * 10 - 1);
+            const int idx = min(tid + kThreads * k, N * 10 - 1);
             const int e = idx / 10, i = idx - 10 * e;
             vm[k] = reinterpret_cast<const float *>(rows.mission + row_of(e) * rows.mission_stride)[i];
         }
 #pragma unroll
         for (int k = 0; k < kScanLoads; ++k) {
-            const int idx = min(tid + kControlThreads * k, 64 * 7 - 1);
+            const int idx = min(tid + kThreads * k, N * 7 - 1);
             const int e = idx / 7, i = idx - 7 * e;
-            vs[k] = rows.prior[row_of(e) * 15 + i];
+            vs[k] = FUSED ? 0.0f : rows.prior[row_of(e) * 15 + i];
         }
         if (SCALARS) {
-            const int idx = min(tid, 64 * 4 - 1);
+            const int idx = min(tid, N * 4 - 1);
             const int e = idx / 4;
             vt = reinterpret_cast<const float *>(
                 rows.obs + row_of(e) * rows.obs_stride)[4144 + idx - 4 * e];
         }
 #pragma unroll
         for (int k = 0; k < kObsLoads; ++k) {
-            const int idx = tid + kControlThreads * k;
+            const int idx = tid + kThreads * k;
             const int e = idx / kStageObs;
-            if (idx < 64 * kStageObs) stage.obs[e][idx - kStageObs * e] = vo[k];
+            if (idx < N * kStageObs) stage.obs[e][idx - kStageObs * e] = vo[k];
         }
 #pragma unroll
         for (int k = 0; k < kMissionLoads; ++k) {
-            const int idx = tid + kControlThreads * k;
+            const int idx = tid + kThreads * k;
             const int e = idx / 10;
-            if (idx < 64 * 10) stage.mission[e][idx - 10 * e] = vm[k];
+            if (idx < N * 10) stage.mission[e][idx - 10 * e] = vm[k];
         }
 #pragma unroll
         for (int k = 0; k < kScanLoads; ++k) {
-            const int idx = tid + kControlThreads * k;
+            const int idx = tid + kThreads * k;
             const int e = idx / 7;
-            if (idx < 64 * 7) stage.scan[e][idx - 7 * e] = vs[k];
+            if (!FUSED && idx < N * 7) stage.scan[e][idx - 7 * e] = vs[k];
         }
-        if (SCALARS && tid < 64 * 4) stage.tail[tid / 4][tid % 4] = vt;
+        if (SCALARS && tid < N * 4) stage.tail[tid / 4][tid % 4] = vt;
         __syncthreads();
+        if constexpr (FUSED) fused_scan(rows, base, stage, fused, w, lane);
 
         // The controller waves take the workgroup's environments BWB
         // missions first, so that all but about one wave of them have no
@@ -1636,8 +1767,8 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
         // environments.  Every environment's values are the same in any
         // order.
         // Tactical waves: environment 16 (w - 4) + lane / 4.
-        int slot = 16 * (w - kControlWaves) + (lane >> 2);
-        if (w < kControlWaves) {
+        int slot = 16 * (w - CW) + (lane >> 2);
+        if (w < CW) {
             const bool b = bwb_mission(stage.mission[lane]);
             const uint64_t bm = __builtin_amdgcn_ballot_w64(b);
             const unsigned nb = (unsigned)__builtin_popcountll(bm);
@@ -1655,7 +1786,7 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
         if (env < rows.batch) {
             const float *obs = stage.obs[slot];
             const float *mission = stage.mission[slot];
-            if (w >= kControlWaves) {
+            if (w >= CW) {
                 // Lane a of the quad writes features 6a .. 6a + 5.
                 float t[6];
                 tactical_quad(obs, mission, a, t);
@@ -1723,7 +1854,7 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
                 }
             }
         }
-        if (SCALARS && w >= kControlWaves) {
+        if (SCALARS && w >= CW) {
             // Lane l's input: obs[l] (l < 48), obs[4144 + l - 48] (l < 52),
             // mission[l - 52] (l < 62).
             const int lo = min(lane, kStageObs - 1), lt = min(max(lane - 48, 0), 3),
@@ -1734,13 +1865,13 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
             float raw[16];
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const int e = 16 * (w - kControlWaves) + j;
+                const int e = 16 * (w - CW) + j;
                 raw[j] = lane < 48 ? stage.obs[e][lo]
                                    : (lane < 52 ? stage.tail[e][lt] : stage.mission[e][lm]);
             }
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const size_t env = base + (size_t)(16 * (w - kControlWaves) + j);
+                const size_t env = base + (size_t)(16 * (w - CW) + j);
                 const bool valid = env < rows.batch;
                 const size_t row = valid ? env : base;
                 actor_scalars(raw[j], lane, rows.proprio + row * 91, rows.mission_vec + row * 49,
@@ -1749,7 +1880,7 @@ __global__ __launch_bounds__(kControlThreads) void onboard_control_kernel(Onboar
         }
 
         // The stage is reused by this workgroup's next 64 environments.
-        if (base + (size_t)gridDim.x * 64 < rows.batch) __syncthreads();
+        if (base + (size_t)gridDim.x * N < rows.batch) __syncthreads();
     }
 }
 
@@ -1772,9 +1903,9 @@ int launch_onboard(const OnboardRows &rows, hipStream_t s, bool pooled) {
     }
     const unsigned ctrl_blocks = ctrl_want > kControlBlocks ? kControlBlocks : (unsigned)ctrl_want;
     if (rows.proprio)
-        onboard_control_kernel<true><<<ctrl_blocks, kControlThreads, 0, s>>>(rows);
+        onboard_control_kernel<true, false><<<ctrl_blocks, kControlThreads, 0, s>>>(rows);
     else
-        onboard_control_kernel<false><<<ctrl_blocks, kControlThreads, 0, s>>>(rows);
+        onboard_control_kernel<false, false><<<ctrl_blocks, kControlThreads, 0, s>>>(rows);
     return hipGetLastError() == hipSuccess;
 }
 
@@ -1798,6 +1929,13 @@ extern "C" int tb_hip_onboard_tactical_prior_device(const float *obs, const floa
     rows.lidar = nullptr;
     rows.batch = batch_size;
     (void)hipGetLastError();
+    if (batch_size >= kFusedMinBatch && batch_size <= kFusedMaxBatch) {
+        // One round of 64-environment workgroups, one per CU.
+        onboard_control_kernel<false, true>
+            <<<(unsigned)((batch_size + 63) / 64), kControlThreads, 0,
+               reinterpret_cast<hipStream_t>(stream)>>>(rows);
+        return hipGetLastError() == hipSuccess;
+    }
     return launch_onboard(rows, reinterpret_cast<hipStream_t>(stream),
                           batch_size >= kPoolMinBatch);
 }
