@@ -1616,10 +1616,16 @@ __device__ __forceinline__ void fused_scan(const OnboardRows &rows, size_t base,
         const int need = rows.diag ? kNeedAll : scan_need(v.m4, v.m5);
         const bool entered = valid && need != kNeedNone;
         if (valid && !entered) stage_result(e, ScanResult{30.0f, 0.0f, 0.0f, 30.0f, 0.0f, -1, 0, 0});
-        const uint64_t m = __builtin_amdgcn_ballot_w64(entered);
+        // Corridor scans (the longest) first.
+        const bool front = (need & kNeedCorridor) != 0;
+        const uint64_t mf = __builtin_amdgcn_ballot_w64(entered && front);
+        const uint64_t mb = __builtin_amdgcn_ballot_w64(entered && !front);
+        const uint64_t m = mf | mb;
         if (entered) {
-            PoolEntry &p = fused.pool[__builtin_amdgcn_mbcnt_hi(
-                (unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u))];
+            const uint64_t mine = front ? mf : mb;
+            const unsigned rank = __builtin_amdgcn_mbcnt_hi(
+                (unsigned)(mine >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)mine, 0u));
+            PoolEntry &p = fused.pool[(front ? 0u : (unsigned)__builtin_popcountll(mf)) + rank];
             p.env = (unsigned)e;
             p.need = need;
 #pragma unroll
