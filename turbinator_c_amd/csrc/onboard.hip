@@ -1380,7 +1380,8 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
 // depends only on its environment.  A static share of the environments
 // would leave the waves that drew several slalom missions working long after
 // the others: at 16,384 environments (four per wave) that wave sets the
-// kernel's time.
+// kernel's time.  The onboard entry uses this kernel from 2,560
+// environments, except for the batches that the one-kernel form takes.
 constexpr int kPoolThreads = 1024;
 constexpr int kPoolWaves = kPoolThreads / 64;
 constexpr int kPoolRound = kPoolThreads;  // environments per round, one per thread
@@ -1548,7 +1549,8 @@ struct ControlStage {
 };
 
 // Phase 2: the tactical features and the controller, from the parked scan
-// result.  A workgroup covers 64 environments: waves 0..3 run the
+// result (FUSED: from the workgroup's own scan, phase 1 and 2 in one
+// kernel).  A workgroup covers 64 environments: waves 0..3 run the
 // controller and waves 4..7 the tactical features, each on one quad of lanes
 // per environment (16 per wave), so every SIMD holds one wave of each.
 // Both are long scalar chains and few waves exist per launch, so splitting
