@@ -400,6 +400,45 @@ def test_scan_forms_agree(torch_cuda, hip, n):
                 f"{np.argwhere((g != w[:n - 1]).any(1))[:5].ravel()}"
 
 
+@pytest.mark.parametrize("variant", [synth.SPECIAL, synth.CLAMP_LIMITS, synth.TIED_MINIMA,
+                                     synth.EDGE_QUARTERS, synth.NO_RETURN])
+def test_one_kernel_form_on_variants(torch_cuda, hip, variant):
+    """The one-kernel form (10,240 to 16,384 environments) on the generator's
+    adversarial variants (NaN / +-Inf / +-0 / 3e38 inputs, clamp limits,
+    tied minima, edge quarters, no returns), ranges scaled into the scan
+    window: 4,096 distinct environments tiled three times on the device must
+    give, row for row, the bits of the 4,096-row call (the pooled scan kernel
+    and the control kernel), with and without diagnostics."""
+    torch = torch_cuda
+    distinct, reps = 4096, 3
+    note(f"onboard one-kernel form, variant {variant}, {distinct * reps} envs")
+    b = synth.make_batch(distinct, seed=5300 + variant, variant=variant, threads=16)
+    obs = torch.from_numpy(in_window(b.obs)).cuda()
+    mission = torch.from_numpy(b.mission).cuda()
+    big_obs = obs.repeat(reps, 1).contiguous()
+    big_mis = mission.repeat(reps, 1).contiguous()
+
+    def run(o, m, with_diag):
+        n = o.shape[0]
+        tac = torch.full((n, 24), float("nan"), dtype=torch.float32, device="cuda")
+        pri = torch.full((n, 15), float("nan"), dtype=torch.float32, device="cuda")
+        diag = torch.full((n, oracle.ONBOARD_DIAG), float("nan"), dtype=torch.float32,
+                          device="cuda") if with_diag else None
+        s = torch.cuda.current_stream()
+        torch.cuda.synchronize()
+        assert hip.onboard_tactical_prior_device(o, m, tac, pri, diag, n, s) == 1
+        assert hip.synchronize(s) == 1
+        return [x for x in (tac, pri, diag) if x is not None]
+
+    for with_diag in (True, False):
+        small = run(obs, mission, with_diag)
+        big = run(big_obs, big_mis, with_diag)
+        for g, w in zip(big, small):
+            w = w.repeat(reps, 1)
+            assert torch.equal(g.view(torch.int32), w.view(torch.int32)), \
+                f"variant {variant} diag {with_diag}: rows differ"
+
+
 def test_more_than_64_environments_per_scan_wave(torch_cuda, hip):
     """The onboard entry's scan takes up to 1,024 environments per workgroup
     and round (256 workgroups), so a batch beyond 262,144 makes every
