@@ -303,14 +303,19 @@ def _leg_onboard(torch, sets, steps, out, tac, pri):
         dodge = m5 > 0.75
         ray_bytes.append(float(np.where(slalom, 4 * 1536, np.where(dodge, 4 * 1024, 0)).mean()))
     onboard_bytes = int(round(fixed + sum(ray_bytes) / len(ray_bytes)))
-    out.append(_report("onboard tactical+prior (16,384 envs)",
-                       _events_time(torch, onboard_call, steps, SUITE_WARMUP), BATCH,
+    per_call = _events_time(torch, onboard_call, steps, SUITE_WARMUP)
+    full_gbs = full_scan * BATCH / per_call / 1e9
+    out.append(_report("onboard tactical+prior (16,384 envs)", per_call, BATCH,
                        onboard_bytes, full_scan_bytes_per_env=full_scan,
+                       full_scan_GBs=round(full_gbs, 1),
+                       full_scan_frac_of_peak=round(full_gbs / HBM_PEAK_GBS, 4),
                        note="bytes_per_env: proprio and mission read once, tactical and "
                             "prior written once, and the scan rays each environment's "
                             "mission uses (rows 0-3 for dodge, all for slalom, none "
                             "otherwise; this batch's average); full_scan_bytes_per_env "
-                            "counts every scan ray; latency-bound, not HBM-bound"))
+                            "counts every scan ray, as the reference's loop reads them "
+                            "(onboard_features.cuh:188-234), and full_scan_GBs is that "
+                            "count over the measured time; latency-bound, not HBM-bound"))
 
 
 def _leg_actor_prep(torch, sets, steps, out, tac, pri):
