@@ -1271,6 +1271,18 @@ __device__ __forceinline__ void actor_scalars(float raw, int lane, float *propri
         lane >= 52 && lane < 62 ? 4 * (lane - 52) : kPastRecords, 0, 0);
 }
 
+// A scan result parked in its environment's prior row (7 of its 15 words)
+// until the control kernel has read it.
+__device__ __forceinline__ void park_scan(float *park, const ScanResult &s) {
+    park[0] = s.min_r;
+    park[1] = s.min_r_dx;
+    park[2] = s.min_r_dy;
+    park[3] = s.min_dx_c;
+    park[4] = s.cluster_y_sum;
+    park[5] = __int_as_float(s.min_ray);
+    park[6] = __int_as_float(s.cluster_count);
+}
+
 // Phase 1 of the actor entry.  Each wave scans one environment at a time;
 // workgroups are persistent (the ray table is loaded into LDS once per
 // workgroup, the only barrier).  Wave g of the grid takes environments g,
@@ -1346,16 +1358,7 @@ __global__ __launch_bounds__(kBlockThreads) void onboard_scan_kernel(OnboardRows
         ScanResult s;
         scan_env(rg, rays, f, next, next_upper, lane, lists[__builtin_amdgcn_readfirstlane(tid >> 6)],
                  s, need);
-        if (lane == 0) {
-            float *park = rows.prior + env * 15;
-            park[0] = s.min_r;
-            park[1] = s.min_r_dx;
-            park[2] = s.min_r_dy;
-            park[3] = s.min_dx_c;
-            park[4] = s.cluster_y_sum;
-            park[5] = __int_as_float(s.min_ray);
-            park[6] = __int_as_float(s.cluster_count);
-        }
+        if (lane == 0) park_scan(rows.prior + env * 15, s);
         if (!has_next) break;
         env = next_env;
         if (++k == 64) {  // the next 64 environments of this wave
@@ -1407,16 +1410,6 @@ struct PoolEntry {
     int need;
     float r[9], py;
 };
-
-__device__ __forceinline__ void park_scan(float *park, const ScanResult &s) {
-    park[0] = s.min_r;
-    park[1] = s.min_r_dx;
-    park[2] = s.min_r_dy;
-    park[3] = s.min_dx_c;
-    park[4] = s.cluster_y_sum;
-    park[5] = __int_as_float(s.min_ray);
-    park[6] = __int_as_float(s.cluster_count);
-}
 
 __global__ __launch_bounds__(kPoolThreads) void onboard_scan_pool_kernel(OnboardRows rows) {
     __shared__ RayPlanes rays;
