@@ -1283,7 +1283,8 @@ __device__ __forceinline__ void park_scan(float *park, const ScanResult &s) {
     park[6] = __int_as_float(s.cluster_count);
 }
 
-// Phase 1 of the actor entry.  Each wave scans one environment at a time;
+// Phase 1 of the actor entry, and of the onboard entry below 2,560
+// environments.  Each wave scans one environment at a time;
 // workgroups are persistent (the ray table is loaded into LDS once per
 // workgroup, the only barrier).  Wave g of the grid takes environments g,
 // g + W, g + 2W, ... (W waves in the grid).  Their scan frames (attitude
