@@ -282,6 +282,20 @@ def _leg_diag(torch, sets, steps, out):
                        BYTES_PER_ENV + diag_bytes))
 
 
+def onboard_scan_ray_bytes(mission: np.ndarray) -> np.ndarray:
+    """Bytes of scan rays each environment's mission uses (onboard_features.cuh:
+    107-109, 208-244): rows 0-3 of both heads (1,024 rays) for a dodge
+    mission (m5 > 0.75), all 1,536 for a slalom mission (m4 > 0.75 and
+    m5 <= 0.25), none otherwise; mission values map NaN -> 0, +-inf -> +-1
+    first (onboard_features.cuh:13-15)."""
+    mis = np.nan_to_num(np.asarray(mission, np.float32)[:, 4:6], nan=0.0, posinf=1.0,
+                        neginf=-1.0)
+    m4, m5 = mis[:, 0], mis[:, 1]
+    slalom = (m4 > 0.75) & (m5 <= 0.25)
+    dodge = m5 > 0.75
+    return np.where(slalom, 4 * 1536, np.where(dodge, 4 * 1024, 0))
+
+
 def _leg_onboard(torch, sets, steps, out, tac, pri):
     from turbinator_c_amd import features
 
@@ -295,13 +309,7 @@ def _leg_onboard(torch, sets, steps, out, tac, pri):
     # m5 <= 0.25), none otherwise (onboard_features.cuh:208-244).
     fixed = 4 * (48 + 10 + 24 + 15)
     full_scan = fixed + 4 * 1536
-    ray_bytes = []
-    for _, m, _, _ in sets:
-        mis = np.nan_to_num(m[:, 4:6].cpu().numpy(), nan=0.0, posinf=1.0, neginf=-1.0)
-        m4, m5 = mis[:, 0], mis[:, 1]
-        slalom = (m4 > 0.75) & (m5 <= 0.25)
-        dodge = m5 > 0.75
-        ray_bytes.append(float(np.where(slalom, 4 * 1536, np.where(dodge, 4 * 1024, 0)).mean()))
+    ray_bytes = [float(onboard_scan_ray_bytes(m.cpu().numpy()).mean()) for _, m, _, _ in sets]
     onboard_bytes = int(round(fixed + sum(ray_bytes) / len(ray_bytes)))
     per_call = _events_time(torch, onboard_call, steps, SUITE_WARMUP)
     full_gbs = full_scan * BATCH / per_call / 1e9
