@@ -337,7 +337,7 @@ def test_scan_uses_by_mission(torch_cuda, hip, variant):
 
 @pytest.mark.parametrize("n,classes", [(2560, "mixed"), (2561, "mixed"), (4097, "mixed"),
                                        (10240, "mixed"), (16384, "slalom"), (16384, "dodge"),
-                                       (16385, "mixed")])
+                                       (16384, "bwb"), (16385, "mixed")])
 def test_pooled_scan_sizes(torch_cuda, hip, n, classes):
     """The H2 entry's scan forms by batch: from 2,560 environments the scan
     kernel shares each workgroup's environments out from a pool in LDS, with
@@ -347,7 +347,9 @@ def test_pooled_scan_sizes(torch_cuda, hip, n, classes):
     17).  From 10,240 to 16,384 environments one kernel scans and controls
     each workgroup's 64 environments: its smallest batch, and full batches
     whose every mission uses the corridor scan or the closest return (the
-    pool holds every environment).  16,385 goes back to two kernels.
+    pool holds every environment) or is a BWB mission that uses no scan
+    result (every controller wave runs the BWB blocks).  16,385 goes back to
+    two kernels.
     Without diagnostics the call must equal the call with them bit for bit,
     and both the oracle on a sample."""
     note(f"onboard pooled scan, {n} envs, {classes} missions")
@@ -359,6 +361,10 @@ def test_pooled_scan_sizes(torch_cuda, hip, n, classes):
         for c, (m4, m5) in enumerate(MISSION_CLASSES):
             mission[cls == c, 4] = m4
             mission[cls == c, 5] = m5
+    elif classes == "bwb":
+        # BWB cruise (m4 > 0.75, m2 > 0.25) with m5 = 0.5 (lateral: no scan
+        # result used), so every controller wave runs the BWB blocks.
+        mission[:, 2], mission[:, 4], mission[:, 5] = 0.5, 1.0, 0.5
     else:
         mission[:, 4], mission[:, 5] = (1.0, 0.0) if classes == "slalom" else (0.0, 1.0)
     full = run_onboard(torch_cuda, hip, obs, mission, with_diag=True)
